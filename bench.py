@@ -1,0 +1,265 @@
+#!/usr/bin/env python3
+"""Attention TFLOP/s of the HIP kernel on one MI355X.
+
+Default workload: one GPU's Ulysses head shard of a 480p/5s MiniMax H3 DiT
+block — B=1, H=5, S=49,920 (32 x 30 x 52 latent tokens), D=128, non-causal,
+bf16; q/k are seeded N(0,1), then RMSNorm (unit gain) + 3D RoPE through the
+HIP prologue, v is N(0,1). A step is one attention forward over that batch;
+TFLOP/s = 4 * S^2 * D * H / t.
+
+Prints one JSON line with the metric, the kernel's roofline position (HIP
+events around every timed launch on the launch stream), the prologue's HBM
+rate, and the reference's CPU path (torch SDPA on host bf16 tensors, the call
+form of benchmarks/benchmark_dense_fa4.py:70-77) timed on a bounded sample of
+query rows on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import re
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "attn TFLOP/s + % bf16 MFMA peak, S=49,920 H=5 D=128 non-causal, 1 MI355X"
+PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA: 256 CU x 4 SIMD x 1024 flop/clk x 2.4 GHz
+PEAK_HBM_GBS = 8000.0
+PMC_SUMMARY = ROOT / "profiles" / "attn_fwd_c2_pmc.txt"
+
+
+def parse_args(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
+    p.add_argument("--cpu-rows", type=int, default=4096, help="query rows in the CPU baseline sample")
+    p.add_argument("--cpu-repeats", type=int, default=3)
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args(argv)
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(torch, q, k, v, heads, rows: int, repeats: int) -> dict:
+    """torch SDPA (the reference's CPU path) on host bf16 tensors, first
+    ``rows`` query rows against every key of every head."""
+
+    from torch.nn import functional
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    rows = min(rows, q.shape[1])
+    qs = q[:, :rows].cpu()
+    kc, vc = k.cpu(), v.cpu()
+
+    def call():
+        return functional.scaled_dot_product_attention(
+            qs.transpose(1, 2), kc.transpose(1, 2), vc.transpose(1, 2), dropout_p=0.0, is_causal=False
+        ).transpose(1, 2)
+
+    call()  # warm-up outside the samples
+    samples = []
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        call()
+        samples.append(time.perf_counter() - t0)
+    med = statistics.median(samples)
+    flops = 4.0 * rows * kc.shape[1] * q.shape[-1] * heads
+    return {
+        "value": flops / med / 1e12,
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "reference",
+        "sample": (
+            f"torch {torch.__version__} F.scaled_dot_product_attention on CPU bf16, first {rows} query rows x "
+            f"{kc.shape[1]} keys x {heads} heads (4*rows*S*D*H = {flops:.3e} flop), median of {repeats} "
+            f"after 1 warm-up ({', '.join(f'{s:.2f}' for s in samples)} s); host {cpu_model()}, "
+            f"{cores} cores in affinity"
+        ),
+    }
+
+
+def read_pmc_traffic() -> dict | None:
+    """HBM bytes per attention launch from the committed rocprofv3 PMC summary."""
+
+    if not PMC_SUMMARY.is_file():
+        return None
+    text = PMC_SUMMARY.read_text()
+    out = {}
+    for key in ("hbm_read_bytes_per_launch", "hbm_write_bytes_per_launch"):
+        m = re.search(rf"^{key}:\s*([0-9.eE+]+)", text, flags=re.M)
+        if m is None:
+            return None
+        out[key] = float(m.group(1))
+    return out
+
+
+def main(argv=None) -> int:
+    args = parse_args(argv)
+    if args.gpus != 1:
+        print(
+            "bench.py measures one MI355X: the attention runs one GPU's head shard and this build "
+            f"launches no collectives; --gpus {args.gpus} is not supported (use --gpus 1).",
+            file=sys.stderr,
+        )
+        return 2
+
+    import torch
+
+    from h3_flash_amd import flash_attn_func
+    from h3_flash_amd.prologue import fused_qk_norm_rope
+    from h3_flash_amd.synth import WORKLOADS, make_raw
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    w = WORKLOADS[args.workload]
+    raw = make_raw(w)
+    q_raw, k_raw, v = raw["q_raw"].to(dev), raw["k_raw"].to(dev), raw["v"].to(dev)
+    cu = raw["cu_seqlens"].to(dev) if raw["cu_seqlens"] is not None else None
+    kw = {} if cu is None else {"cu_seqlens_q": cu, "cu_seqlens_k": cu, "max_seqlen_q": max(w.segments)}
+    stream = torch.cuda.current_stream(dev)
+
+    prologue = None
+    if w.prologue:
+        cos, sin = raw["cos"].to(dev), raw["sin"].to(dev)
+        wq, wk = raw["w_q"].to(dev), raw["w_k"].to(dev)
+
+        def run_prologue():
+            return fused_qk_norm_rope(q_raw, k_raw, wq, wk, cos, sin, raw["eps"], raw["eps"])
+
+        q, k = run_prologue()
+        for _ in range(3):
+            run_prologue()
+        torch.cuda.synchronize()
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
+        for a, b in evs:
+            a.record(stream)
+            run_prologue()
+            b.record(stream)
+        torch.cuda.synchronize()
+        pro_ms = statistics.fmean(a.elapsed_time(b) for a, b in evs)
+        S, H, D, R = w.seqlen, w.heads, w.head_dim, cos.shape[1]
+        pro_bytes = 2 * (2 * S * H * D * 2) + 2 * S * R * 4
+        prologue = {
+            "kernel": "qknorm_rope_kernel (q and k in one launch)",
+            "ms": pro_ms,
+            "bytes_per_launch": pro_bytes,
+            "GB_s": pro_bytes / (pro_ms * 1e-3) / 1e9,
+            "frac_of_hbm_peak": pro_bytes / (pro_ms * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        }
+    else:
+        q, k = q_raw, k_raw
+    del q_raw, k_raw
+
+    out = torch.empty_like(q)
+    lse = torch.empty((w.batch, w.heads, w.seqlen), dtype=torch.float32, device=dev)
+
+    def step():
+        flash_attn_func(q, k, v, out=out, lse=lse, **kw)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    region0 = torch.cuda.Event(enable_timing=True)
+    region1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    region0.record(stream)
+    for a, b in events:
+        a.record(stream)
+        step()
+        b.record(stream)
+    region1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    region_ms = region0.elapsed_time(region1)
+    launch_ms = [a.elapsed_time(b) for a, b in events]
+    ms_per_step = region_ms / args.steps
+    kernel_ms = statistics.fmean(launch_ms)
+
+    flops = w.flops
+    value = flops / (ms_per_step * 1e-3) / 1e12
+    achieved = flops / (kernel_ms * 1e-3) / 1e12
+    traffic = read_pmc_traffic()
+    compulsory = 2 * (2 * w.seqlen * w.heads * w.head_dim * 2) + w.seqlen * w.heads * 4
+
+    result = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) q/k -> HIP qk-RMSNorm (unit gain) + 3D RoPE; v N(0,1)"
+        if w.prologue
+        else "synthetic: seeded N(0,1) q/k/v",
+        "config": {
+            "workload": f"dense non-causal attention, {w.describe()}"
+            + (f", packed segments {list(w.segments)}" if w.varlen else "")
+            + ("; one Ulysses head shard of a 480p/5s H3 DiT block" if args.workload == "c2" else ""),
+            "batch": w.batch,
+            "heads": w.heads,
+            "seq_len": w.seqlen,
+            "head_dim": w.head_dim,
+            "causal": False,
+            "parallelism": "single GPU (one head shard, no collectives)",
+        },
+        "pct_of_peak": 100.0 * value / PEAK_BF16_TFLOPS,
+        "roofline": {
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / PEAK_BF16_TFLOPS,
+            "traffic": (traffic["hbm_read_bytes_per_launch"] + traffic["hbm_write_bytes_per_launch"])
+            if traffic
+            else None,
+            "kernel": "attn_fwd_kernel",
+            "kernel_ms_mean": kernel_ms,
+            "kernel_ms_min": min(launch_ms),
+            "algorithmic_flop_per_launch": flops,
+            "compulsory_hbm_bytes_per_launch": compulsory,
+        },
+        "prologue": prologue,
+        "wall_s_timed_region": wall,
+        "device": torch.cuda.get_device_name(0),
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch, q, k, v, w.heads, args.cpu_rows, args.cpu_repeats)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    if not math.isfinite(value):
+        return 1
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,82 @@
+"""Compile the gfx950 HIP library ``_lib/libh3attn.so`` in-tree.
+
+Run as ``python -m h3_flash_amd._build``. The library is the only native
+artefact of the package; the Python side binds it through ctypes.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PACKAGE_DIR = Path(__file__).resolve().parent
+REPO_DIR = PACKAGE_DIR.parent
+CSRC_DIR = PACKAGE_DIR / "csrc"
+LIB_DIR = PACKAGE_DIR / "_lib"
+LIB_PATH = LIB_DIR / "libh3attn.so"
+INCLUDE_DIR = REPO_DIR / "include"
+
+SOURCES = ("capi.hip", "attn_fwd.hip", "qknorm_rope.hip")
+
+HIPCC_FLAGS = (
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-fvisibility=hidden",
+    # Packed fp32 VALU forms stay disabled: only scalar fp32 VALU is emitted.
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+)
+
+
+def hipcc() -> str:
+    """Path of hipcc (ROCM_PATH/bin first, then PATH)."""
+    root = os.environ.get("ROCM_PATH", "/opt/rocm")
+    candidate = Path(root) / "bin" / "hipcc"
+    if candidate.is_file():
+        return str(candidate)
+    found = shutil.which("hipcc")
+    if found is None:
+        raise RuntimeError("hipcc not found: set ROCM_PATH or put hipcc on PATH")
+    return found
+
+
+def build_library(verbose: bool = False, extra_flags: tuple[str, ...] = ()) -> Path:
+    """Compile every HIP source into ``_lib/libh3attn.so`` and return its path.
+
+    The output is written to a temporary name and renamed, so a concurrent
+    reader never sees a half-written library.
+    """
+
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [
+        hipcc(),
+        *HIPCC_FLAGS,
+        *extra_flags,
+        f"-I{INCLUDE_DIR}",
+        *(str(CSRC_DIR / name) for name in SOURCES),
+        "-o",
+        str(tmp),
+    ]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(
+            f"hipcc failed ({result.returncode}):\n{result.stdout}\n{result.stderr}"
+        )
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    path = build_library(verbose="-v" in sys.argv)
+    print(path)

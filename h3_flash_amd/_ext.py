@@ -1,0 +1,144 @@
+"""ctypes binding of the C ABI in ``include/h3attn.h``.
+
+The structures below mirror ``h3a_attn_args`` and ``h3a_qknorm_rope_args``
+field for field. Loading fails loudly (``RuntimeError``) when the library has
+not been built: there is no other implementation behind these entry points.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import threading
+from pathlib import Path
+
+from ._build import LIB_PATH
+
+ABI_VERSION = 1
+
+H3A_OK = 0
+H3A_EINVAL = -1
+H3A_EUNSUPPORTED = -2
+H3A_ELAUNCH = -3
+
+H3A_DTYPE_BF16 = 0
+H3A_DTYPE_F32 = 1
+
+_I64x3 = ctypes.c_int64 * 3
+_I64x2 = ctypes.c_int64 * 2
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("o", ctypes.c_void_p),
+        ("lse", ctypes.c_void_p),
+        ("batch", ctypes.c_int64),
+        ("heads", ctypes.c_int64),
+        ("seqlen_q", ctypes.c_int64),
+        ("seqlen_k", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("q_stride", _I64x3),
+        ("k_stride", _I64x3),
+        ("v_stride", _I64x3),
+        ("o_stride", _I64x3),
+        ("lse_stride", _I64x2),
+        ("softmax_scale", ctypes.c_float),
+        ("causal", ctypes.c_int32),
+        ("cu_seqlens_q", ctypes.c_void_p),
+        ("cu_seqlens_k", ctypes.c_void_p),
+        ("num_segments", ctypes.c_int32),
+        ("max_seqlen_q", ctypes.c_int32),
+    ]
+
+
+class QkNormRopeArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("xq", ctypes.c_void_p),
+        ("xk", ctypes.c_void_p),
+        ("yq", ctypes.c_void_p),
+        ("yk", ctypes.c_void_p),
+        ("wq", ctypes.c_void_p),
+        ("wk", ctypes.c_void_p),
+        ("w_dtype", ctypes.c_int32),
+        ("cos", ctypes.c_void_p),
+        ("sin", ctypes.c_void_p),
+        ("table_stride", ctypes.c_int64),
+        ("batch", ctypes.c_int64),
+        ("seqlen", ctypes.c_int64),
+        ("heads", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("rotary_dim", ctypes.c_int64),
+        ("xq_stride", _I64x3),
+        ("xk_stride", _I64x3),
+        ("yq_stride", _I64x3),
+        ("yk_stride", _I64x3),
+        ("eps_q", ctypes.c_float),
+        ("eps_k", ctypes.c_float),
+    ]
+
+
+# Every function the header declares, with its ctypes signature.
+SIGNATURES = {
+    "h3a_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
+    "h3a_qknorm_rope": (ctypes.c_int, [ctypes.POINTER(QkNormRopeArgs), ctypes.c_void_p]),
+    "h3a_last_error": (ctypes.c_char_p, []),
+    "h3a_abi_version": (ctypes.c_int, []),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def library_path() -> Path:
+    return LIB_PATH
+
+
+def load_library(path: Path | None = None) -> ctypes.CDLL:
+    """Load (once) and return the HIP library; raise RuntimeError if absent."""
+
+    global _lib
+    target = Path(path) if path is not None else LIB_PATH
+    with _lock:
+        if _lib is not None and path is None:
+            return _lib
+        if not target.is_file():
+            raise RuntimeError(
+                f"HIP attention library not found at {target}; build it with "
+                "`python -m h3_flash_amd._build` (hipcc, gfx950)"
+            )
+        lib = ctypes.CDLL(str(target))
+        for name, (restype, argtypes) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = restype
+            fn.argtypes = argtypes
+        version = lib.h3a_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(
+                f"HIP attention library ABI {version} does not match binding ABI {ABI_VERSION}"
+            )
+        if path is None:
+            _lib = lib
+        return lib
+
+
+def last_error(lib: ctypes.CDLL) -> str:
+    message = lib.h3a_last_error()
+    return message.decode("utf-8", "replace") if message else ""
+
+
+def provenance() -> dict:
+    """Identity of the loaded library, for install-time audit records."""
+
+    lib = load_library()
+    digest = hashlib.sha256(LIB_PATH.read_bytes()).hexdigest()
+    return {
+        "library": str(LIB_PATH),
+        "abi_version": int(lib.h3a_abi_version()),
+        "arch": "gfx950",
+        "sha256": digest,
+    }

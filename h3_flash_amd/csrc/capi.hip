@@ -1,0 +1,168 @@
+// extern "C" entry points declared in include/h3attn.h: argument validation,
+// error reporting and launch of the gfx950 kernels. No allocation, no host
+// synchronisation, no global mutable state besides the per-thread message.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "h3attn.h"
+#include "kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+constexpr int64_t kMaxSpan = (int64_t)1 << 31;  // buffer offsets are 32-bit
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+const char* h3a_last_error(void) { return g_err; }
+
+int h3a_abi_version(void) { return H3A_ABI_VERSION; }
+
+int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
+    g_err[0] = '\0';
+    if (a == nullptr) return fail(H3A_EINVAL, "h3a_attn_fwd: args is NULL");
+    if (a->abi_version != H3A_ABI_VERSION)
+        return fail(H3A_EINVAL, "h3a_attn_fwd: abi_version %d, library is %d", a->abi_version, H3A_ABI_VERSION);
+    if (a->causal != 0) return fail(H3A_EUNSUPPORTED, "h3a_attn_fwd: causal attention is not supported (non-causal path)");
+    if (a->head_dim != 128) return fail(H3A_EUNSUPPORTED, "h3a_attn_fwd: head_dim must be 128, got %lld", (long long)a->head_dim);
+    if (a->batch < 0 || a->heads <= 0 || a->seqlen_q < 0 || a->seqlen_k < 0)
+        return fail(H3A_EINVAL, "h3a_attn_fwd: negative or zero extent (batch=%lld heads=%lld sq=%lld sk=%lld)",
+                    (long long)a->batch, (long long)a->heads, (long long)a->seqlen_q, (long long)a->seqlen_k);
+    if (!(a->softmax_scale > 0.f) || !isfinite(a->softmax_scale))
+        return fail(H3A_EINVAL, "h3a_attn_fwd: softmax_scale must be finite and > 0");
+    if (a->batch == 0 || a->seqlen_q == 0) return H3A_OK;
+    if (!a->q || !a->o || (a->seqlen_k > 0 && (!a->k || !a->v)))
+        return fail(H3A_EINVAL, "h3a_attn_fwd: NULL tensor pointer");
+    if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))
+        return fail(H3A_EINVAL, "h3a_attn_fwd: q/k/v/o must be 16-byte aligned");
+    const int64_t* st[4] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride};
+    const char* nm[4] = {"q", "k", "v", "o"};
+    for (int i = 0; i < 4; ++i) {
+        for (int d = 0; d < 3; ++d)
+            if (st[i][d] < 0 || st[i][d] % 8 != 0)
+                return fail(H3A_EINVAL, "h3a_attn_fwd: %s strides must be non-negative multiples of 8 elements", nm[i]);
+        if (st[i][1] < 128) return fail(H3A_EINVAL, "h3a_attn_fwd: %s sequence stride %lld < head_dim", nm[i], (long long)st[i][1]);
+    }
+
+    const bool varlen = a->cu_seqlens_q != nullptr;
+    int64_t rows_q = a->seqlen_q, rows_k = a->seqlen_k;
+    h3a::AttnParams p{};
+    p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o; p.lse = a->lse;
+    p.q_sb = a->q_stride[0]; p.q_sh = a->q_stride[2];
+    p.k_sb = a->k_stride[0]; p.k_sh = a->k_stride[2];
+    p.v_sb = a->v_stride[0]; p.v_sh = a->v_stride[2];
+    p.o_sb = a->o_stride[0]; p.o_sh = a->o_stride[2];
+    p.lse_sb = a->lse_stride[0]; p.lse_sh = a->lse_stride[1];
+    p.heads = (int32_t)a->heads;
+    p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
+    const int bm = h3a::attn_fwd_block_m();
+    if (varlen) {
+        if (a->cu_seqlens_k == nullptr) return fail(H3A_EINVAL, "h3a_attn_fwd: cu_seqlens_q given without cu_seqlens_k");
+        if (a->batch != 1) return fail(H3A_EINVAL, "h3a_attn_fwd: varlen requires batch == 1, got %lld", (long long)a->batch);
+        if (a->num_segments <= 0) return fail(H3A_EINVAL, "h3a_attn_fwd: num_segments must be > 0");
+        if (a->max_seqlen_q <= 0 || a->max_seqlen_q > a->seqlen_q)
+            return fail(H3A_EINVAL, "h3a_attn_fwd: max_seqlen_q must be in [1, seqlen_q]");
+        p.cu_q = a->cu_seqlens_q;
+        p.cu_k = a->cu_seqlens_k;
+        p.n_groups = a->num_segments;
+        p.n_qtiles = (a->max_seqlen_q + bm - 1) / bm;
+        if (a->seqlen_q > INT32_MAX / 2 || a->seqlen_k > INT32_MAX / 2)
+            return fail(H3A_EINVAL, "h3a_attn_fwd: sequence length too large");
+        p.seqlen_q = (int32_t)a->seqlen_q;  // packed totals; segments are clamped to them
+        p.seqlen_k = (int32_t)a->seqlen_k;
+    } else {
+        if (a->seqlen_q > INT32_MAX / 2 || a->seqlen_k > INT32_MAX / 2)
+            return fail(H3A_EINVAL, "h3a_attn_fwd: sequence length too large");
+        p.cu_q = nullptr; p.cu_k = nullptr;
+        p.n_groups = (int32_t)a->batch;
+        p.n_qtiles = (int32_t)((a->seqlen_q + bm - 1) / bm);
+        p.seqlen_q = (int32_t)a->seqlen_q;
+        p.seqlen_k = (int32_t)a->seqlen_k;
+    }
+    // Every (batch, head) view is addressed with 32-bit byte offsets that may
+    // run up to one tile past the last row.
+    const int64_t rows[4] = {rows_q, rows_k, rows_k, rows_q};
+    for (int i = 0; i < 4; ++i) {
+        const int64_t span = (rows[i] + bm + 64) * st[i][1] * 2;
+        if (span >= kMaxSpan)
+            return fail(H3A_EUNSUPPORTED, "h3a_attn_fwd: %s view spans %lld bytes (limit 2^31)", nm[i], (long long)span);
+    }
+    p.q_rs = (int32_t)(a->q_stride[1] * 2);
+    p.k_rs = (int32_t)(a->k_stride[1] * 2);
+    p.v_rs = (int32_t)(a->v_stride[1] * 2);
+    p.o_rs = (int32_t)(a->o_stride[1] * 2);
+    const int64_t blocks = (int64_t)p.n_qtiles * p.heads * p.n_groups;
+    if (blocks > INT32_MAX) return fail(H3A_EUNSUPPORTED, "h3a_attn_fwd: grid too large");
+    hipError_t e = h3a::launch_attn_fwd(p, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_attn_fwd: launch failed: %s", hipGetErrorString(e));
+    return H3A_OK;
+}
+
+int h3a_qknorm_rope(const h3a_qknorm_rope_args* a, void* stream) {
+    g_err[0] = '\0';
+    if (a == nullptr) return fail(H3A_EINVAL, "h3a_qknorm_rope: args is NULL");
+    if (a->abi_version != H3A_ABI_VERSION)
+        return fail(H3A_EINVAL, "h3a_qknorm_rope: abi_version %d, library is %d", a->abi_version, H3A_ABI_VERSION);
+    const int64_t D = a->head_dim, R = a->rotary_dim;
+    if (R > D || R % 2 != 0 || R < 0)
+        return fail(H3A_EINVAL,
+                    "fused qknorm+rope requires an even rotary dimension no wider than the head, got rotary_dim=%lld, "
+                    "head_dim=%lld",
+                    (long long)R, (long long)D);
+    if (D <= 0 || D % 8 != 0 || D > 512)
+        return fail(H3A_EUNSUPPORTED, "h3a_qknorm_rope: head_dim must be a multiple of 8 in [8, 512], got %lld", (long long)D);
+    if (a->batch < 0 || a->seqlen < 0 || a->heads <= 0) return fail(H3A_EINVAL, "h3a_qknorm_rope: bad extents");
+    if (a->w_dtype != H3A_DTYPE_BF16 && a->w_dtype != H3A_DTYPE_F32)
+        return fail(H3A_EINVAL, "h3a_qknorm_rope: unknown weight dtype %d", a->w_dtype);
+    if (a->batch == 0 || a->seqlen == 0) return H3A_OK;
+    if (!a->xq || !a->yq || !a->wq) return fail(H3A_EINVAL, "h3a_qknorm_rope: NULL q pointer");
+    const int n = a->xk ? 2 : 1;
+    if (n == 2 && (!a->yk || !a->wk)) return fail(H3A_EINVAL, "h3a_qknorm_rope: xk given without yk/wk");
+    if (R > 0 && (!a->cos || !a->sin)) return fail(H3A_EINVAL, "h3a_qknorm_rope: NULL cos/sin table");
+    if (R > 0 && a->table_stride < R) return fail(H3A_EINVAL, "h3a_qknorm_rope: table_stride < rotary_dim");
+    h3a::QkNormRopeParams p{};
+    const void* xs[2] = {a->xq, a->xk};
+    void* ys[2] = {a->yq, a->yk};
+    const void* ws[2] = {a->wq, a->wk};
+    const int64_t* xst[2] = {a->xq_stride, a->xk_stride};
+    const int64_t* yst[2] = {a->yq_stride, a->yk_stride};
+    const float eps[2] = {a->eps_q, a->eps_k};
+    for (int i = 0; i < n; ++i) {
+        if (!aligned16(xs[i]) || !aligned16(ys[i]) || !aligned16(ws[i]))
+            return fail(H3A_EINVAL, "h3a_qknorm_rope: tensors must be 16-byte aligned");
+        for (int d = 0; d < 3; ++d)
+            if (xst[i][d] % 8 != 0 || yst[i][d] % 8 != 0 || xst[i][d] < 0 || yst[i][d] < 0)
+                return fail(H3A_EINVAL, "h3a_qknorm_rope: strides must be non-negative multiples of 8 elements");
+        p.x[i] = xs[i]; p.y[i] = ys[i]; p.w[i] = ws[i]; p.eps[i] = eps[i];
+        p.x_sb[i] = xst[i][0]; p.x_ss[i] = xst[i][1]; p.x_sh[i] = xst[i][2];
+        p.y_sb[i] = yst[i][0]; p.y_ss[i] = yst[i][1]; p.y_sh[i] = yst[i][2];
+    }
+    if (n == 1) {  // second slot mirrors the first; never selected when n_tensors == 1
+        p.x[1] = p.x[0]; p.y[1] = p.y[0]; p.w[1] = p.w[0]; p.eps[1] = p.eps[0];
+        p.x_sb[1] = p.x_sb[0]; p.x_ss[1] = p.x_ss[0]; p.x_sh[1] = p.x_sh[0];
+        p.y_sb[1] = p.y_sb[0]; p.y_ss[1] = p.y_ss[0]; p.y_sh[1] = p.y_sh[0];
+    }
+    p.cos = a->cos; p.sin = a->sin; p.table_stride = a->table_stride;
+    p.seqlen = (int32_t)a->seqlen; p.heads = (int32_t)a->heads; p.n_tensors = n;
+    p.head_dim = (int32_t)D; p.rotary_dim = (int32_t)R; p.w_f32 = a->w_dtype == H3A_DTYPE_F32;
+    p.rows = a->batch * a->seqlen * n * a->heads;
+    hipError_t e = h3a::launch_qknorm_rope(p, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_qknorm_rope: launch failed: %s", hipGetErrorString(e));
+    return H3A_OK;
+}
+
+}  // extern "C"

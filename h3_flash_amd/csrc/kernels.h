@@ -1,0 +1,56 @@
+// Internal launch interface between the C ABI (capi.hip) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace h3a {
+
+// Validated attention launch description. Strides are in elements.
+struct AttnParams {
+    const void* q;
+    const void* k;
+    const void* v;
+    void* o;
+    float* lse;
+    int64_t q_sb, q_sh;  // batch / head strides of Q
+    int64_t k_sb, k_sh;
+    int64_t v_sb, v_sh;
+    int64_t o_sb, o_sh;
+    int64_t lse_sb, lse_sh;
+    int32_t q_rs, k_rs, v_rs, o_rs;  // sequence (row) strides, in bytes
+    int32_t heads;
+    int32_t seqlen_q;  // dense: per-batch lengths; varlen: packed row totals
+    int32_t seqlen_k;
+    int32_t n_qtiles;  // query tiles per (batch-or-segment, head)
+    int32_t n_groups;  // batch (dense) or number of segments (varlen)
+    float scale_log2;  // softmax_scale * log2(e)
+    const int32_t* cu_q;  // NULL for dense
+    const int32_t* cu_k;
+};
+
+int attn_fwd_block_m();
+hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream);
+
+struct QkNormRopeParams {
+    const void* x[2];
+    void* y[2];
+    const void* w[2];
+    float eps[2];
+    int64_t x_sb[2], x_ss[2], x_sh[2];
+    int64_t y_sb[2], y_ss[2], y_sh[2];
+    const float* cos;
+    const float* sin;
+    int64_t table_stride;
+    int64_t rows;  // batch * seqlen * n_tensors * heads
+    int32_t seqlen;
+    int32_t heads;
+    int32_t n_tensors;  // 1 (q only) or 2 (q and k)
+    int32_t head_dim;
+    int32_t rotary_dim;
+    int32_t w_f32;  // 1: weights are fp32, 0: bf16
+};
+
+hipError_t launch_qknorm_rope(const QkNormRopeParams& p, hipStream_t stream);
+
+}  // namespace h3a

@@ -1,0 +1,149 @@
+/*
+ * h3attn — C ABI of the MI355X (gfx950) dense attention hot path.
+ *
+ * Two device entry points replace the two GPU steps of the reference's dense
+ * attention path inside each MiniMax H3 DiT block:
+ *
+ *   h3a_attn_fwd      replaces the FlashAttention-4 call made by the dense-FA4
+ *                     adapter, `self.kernel(query, key, value, causal=False)`
+ *                     (src/h3_flash/runtime/attention/dense_fa4.py:145, call
+ *                     form at :74-80) and the torch SDPA call of the fused and
+ *                     packed paths (src/h3_flash/runtime/kernels/transformer.py:191-200,
+ *                     src/h3_flash/runtime/parallel/packed_ulysses.py:202-209).
+ *   h3a_qknorm_rope   replaces the Triton `fused_qknorm_rope(x, weight, cos,
+ *                     sin, eps)` (src/h3_flash/runtime/kernels/fusions.py:268-293,
+ *                     kernel :126-175), called once for q and once for k at
+ *                     src/h3_flash/runtime/kernels/transformer.py:160-173; here
+ *                     both tensors are normalised and rotated in one launch.
+ *
+ * Conventions
+ *   - All tensor pointers are device pointers allocated by the caller; the
+ *     library allocates nothing and keeps no per-call state.
+ *   - Strides are in elements. The last (head_dim / rotary) dimension must be
+ *     contiguous.
+ *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream).
+ *     Nothing synchronises the host.
+ *   - Return value: 0 on success, a negative H3A_E* code otherwise; the
+ *     message of the last failure on the calling thread is returned by
+ *     h3a_last_error().
+ *   - Entry points are re-entrant: arguments travel in per-call structs.
+ */
+#ifndef H3ATTN_H
+#define H3ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The library is built with hidden visibility; only these symbols export. */
+#define H3A_API __attribute__((visibility("default")))
+
+#define H3A_ABI_VERSION 1
+
+#define H3A_OK 0
+#define H3A_EINVAL (-1)       /* invalid argument (shape, stride, pointer) */
+#define H3A_EUNSUPPORTED (-2) /* valid request this build does not implement */
+#define H3A_ELAUNCH (-3)      /* the HIP launch itself failed */
+
+/* dtype codes used by h3a_qknorm_rope for the norm weights */
+#define H3A_DTYPE_BF16 0
+#define H3A_DTYPE_F32 1
+
+/*
+ * Dense (or block-diagonal varlen) non-causal attention forward,
+ *   O = softmax(softmax_scale * Q K^T) V,   LSE = logsumexp(softmax_scale * Q K^T)
+ * per (batch, head). Q/K/V/O are bf16 in BSHD layout (batch, seq, head, dim),
+ * head_dim must be 128. LSE is fp32, natural log, laid out (batch, head, seq)
+ * with strides lse_stride[0] (batch), lse_stride[1] (head) and 1 (seq); it may
+ * be NULL when the caller does not want it.
+ *
+ * Varlen: when cu_seqlens_q is non-NULL, batch must be 1 and the sequence
+ * dimension holds `num_segments` packed segments; segment i owns rows
+ * [cu_seqlens_q[i], cu_seqlens_q[i+1]) of Q/O/LSE and rows
+ * [cu_seqlens_k[i], cu_seqlens_k[i+1]) of K/V (cu_seqlens_k may equal
+ * cu_seqlens_q). Both arrays are int32 device arrays of num_segments+1
+ * entries; max_seqlen_q bounds every query segment. Attention is
+ * block-diagonal: a query attends only to keys of its own segment.
+ *
+ * Rows with no key (seqlen_k == 0) produce O = 0 and LSE = -inf.
+ */
+typedef struct h3a_attn_args {
+    int32_t abi_version; /* must be H3A_ABI_VERSION */
+    const void *q;       /* bf16 */
+    const void *k;       /* bf16 */
+    const void *v;       /* bf16 */
+    void *o;             /* bf16 */
+    float *lse;          /* fp32 or NULL */
+    int64_t batch;
+    int64_t heads;
+    int64_t seqlen_q;
+    int64_t seqlen_k;
+    int64_t head_dim;
+    int64_t q_stride[3]; /* batch, seq, head */
+    int64_t k_stride[3];
+    int64_t v_stride[3];
+    int64_t o_stride[3];
+    int64_t lse_stride[2]; /* batch, head */
+    float softmax_scale;
+    int32_t causal; /* must be 0: the path is non-causal */
+    const int32_t *cu_seqlens_q;
+    const int32_t *cu_seqlens_k;
+    int32_t num_segments;
+    int32_t max_seqlen_q;
+} h3a_attn_args;
+
+H3A_API int h3a_attn_fwd(const h3a_attn_args *args, void *stream);
+
+/*
+ * Fused per-head RMSNorm + rotate-half RoPE on q and k in one launch:
+ *   r      = rsqrt(mean(x^2) + eps)            (over head_dim, fp32)
+ *   n[c]   = x[c] * r * w[c]
+ *   y[c]   = n[c]*cos[s,c] - n[c+R/2]*sin[s,c]   c <  R/2
+ *   y[c]   = n[c]*cos[s,c] + n[c-R/2]*sin[s,c]   R/2 <= c < R
+ *   y[c]   = n[c]                               c >= R
+ * stored in bf16. x/y are bf16 in BSHD layout; w is (head_dim,) in bf16 or
+ * fp32 (w_dtype); cos/sin are fp32 (seqlen, R) tables with row stride
+ * table_stride. R must be even and <= head_dim; head_dim a multiple of 8 and
+ * at most 512. xk/yk/wk may be NULL to transform one tensor only. y may alias
+ * x (in place).
+ */
+typedef struct h3a_qknorm_rope_args {
+    int32_t abi_version;
+    const void *xq;
+    const void *xk;
+    void *yq;
+    void *yk;
+    const void *wq;
+    const void *wk;
+    int32_t w_dtype;
+    const float *cos;
+    const float *sin;
+    int64_t table_stride;
+    int64_t batch;
+    int64_t seqlen;
+    int64_t heads;
+    int64_t head_dim;
+    int64_t rotary_dim;
+    int64_t xq_stride[3]; /* batch, seq, head */
+    int64_t xk_stride[3];
+    int64_t yq_stride[3];
+    int64_t yk_stride[3];
+    float eps_q;
+    float eps_k;
+} h3a_qknorm_rope_args;
+
+H3A_API int h3a_qknorm_rope(const h3a_qknorm_rope_args *args, void *stream);
+
+/* Message of the last failed call on this thread ("" if none). */
+H3A_API const char *h3a_last_error(void);
+
+/* H3A_ABI_VERSION of the loaded library. */
+H3A_API int h3a_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* H3ATTN_H */

@@ -1,0 +1,139 @@
+"""The C-ABI library: it loads, exports every entry point include/h3attn.h
+declares, and rejects bad arguments before any device work (runs without a
+GPU: every call here returns from validation)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from h3_flash_amd import _ext
+
+# These calls carry fake device pointers and must return from validation; on a
+# host with a visible GPU a case that slipped through would launch on them, so
+# they only run where no GPU is visible (the GPU tests cover real tensors).
+host_only = pytest.mark.skipif(torch.cuda.is_available(), reason="fake device pointers: GPU-less hosts only")
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "h3attn.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\s\*]+?\b(h3a_\w+)\s*\(", text, flags=re.M)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _ext.load_library()
+
+
+def test_header_declares_the_expected_entry_points():
+    assert declared_functions() == ["h3a_abi_version", "h3a_attn_fwd", "h3a_last_error", "h3a_qknorm_rope"]
+
+
+def test_library_exports_every_declared_function(lib):
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _ext.SIGNATURES, name
+
+
+def test_abi_version(lib):
+    assert lib.h3a_abi_version() == _ext.ABI_VERSION == 1
+
+
+def _attn_args(**overrides):
+    a = _ext.AttnArgs()
+    a.abi_version = _ext.ABI_VERSION
+    a.q = a.k = a.v = a.o = 1 << 20
+    a.batch, a.heads, a.seqlen_q, a.seqlen_k, a.head_dim = 1, 1, 16, 16, 128
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        getattr(a, name)[:] = (16 * 128, 128, 128)
+    a.lse_stride[:] = (16, 16)
+    a.softmax_scale = 0.088
+    for k, v in overrides.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "overrides, code, message",
+    [
+        ({"abi_version": 7}, _ext.H3A_EINVAL, "abi_version"),
+        ({"causal": 1}, _ext.H3A_EUNSUPPORTED, "causal"),
+        ({"head_dim": 64}, _ext.H3A_EUNSUPPORTED, "head_dim must be 128"),
+        ({"heads": 0}, _ext.H3A_EINVAL, "extent"),
+        ({"softmax_scale": 0.0}, _ext.H3A_EINVAL, "softmax_scale"),
+        ({"softmax_scale": float("nan")}, _ext.H3A_EINVAL, "softmax_scale"),
+        ({"q": None}, _ext.H3A_EINVAL, "NULL"),
+        ({"k": (1 << 20) + 4}, _ext.H3A_EINVAL, "aligned"),
+        ({"batch": 2, "cu_seqlens_q": 1 << 20, "cu_seqlens_k": 1 << 20, "num_segments": 1, "max_seqlen_q": 8},
+         _ext.H3A_EINVAL, "batch == 1"),
+        ({"cu_seqlens_q": 1 << 20, "num_segments": 1, "max_seqlen_q": 8}, _ext.H3A_EINVAL, "cu_seqlens_k"),
+        ({"cu_seqlens_q": 1 << 20, "cu_seqlens_k": 1 << 20, "num_segments": 1, "max_seqlen_q": 99},
+         _ext.H3A_EINVAL, "max_seqlen_q"),
+        ({"seqlen_q": 1 << 23, "seqlen_k": 1 << 23}, _ext.H3A_EUNSUPPORTED, "2^31"),
+    ],
+)
+@host_only
+def test_attn_validation(lib, overrides, code, message):
+    a = _attn_args(**overrides)
+    rc = lib.h3a_attn_fwd(ctypes.byref(a), None)
+    assert rc == code
+    assert message in _ext.last_error(lib)
+
+
+@host_only
+def test_attn_bad_strides(lib):
+    a = _attn_args()
+    a.k_stride[:] = (16 * 128, 100, 128)
+    assert lib.h3a_attn_fwd(ctypes.byref(a), None) == _ext.H3A_EINVAL
+    a = _attn_args()
+    a.v_stride[:] = (16 * 128, 132, 4)
+    assert lib.h3a_attn_fwd(ctypes.byref(a), None) == _ext.H3A_EINVAL
+
+
+@host_only
+def test_attn_null_args_and_empty_problem(lib):
+    assert lib.h3a_attn_fwd(None, None) == _ext.H3A_EINVAL
+    # empty problems return before any device work
+    assert lib.h3a_attn_fwd(ctypes.byref(_attn_args(seqlen_q=0)), None) == _ext.H3A_OK
+    assert lib.h3a_attn_fwd(ctypes.byref(_attn_args(batch=0)), None) == _ext.H3A_OK
+    assert _ext.last_error(lib) == ""
+
+
+def _rope_args(**overrides):
+    a = _ext.QkNormRopeArgs()
+    a.abi_version = _ext.ABI_VERSION
+    a.xq = a.yq = a.wq = 1 << 20
+    a.cos = a.sin = 1 << 21
+    a.table_stride = 128
+    a.batch, a.seqlen, a.heads, a.head_dim, a.rotary_dim = 1, 4, 2, 128, 128
+    a.xq_stride[:] = a.yq_stride[:] = (4 * 2 * 128, 2 * 128, 128)
+    a.eps_q = a.eps_k = 1e-5
+    for k, v in overrides.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "overrides, code, message",
+    [
+        ({"rotary_dim": 3}, _ext.H3A_EINVAL, "even rotary dimension no wider than the head"),
+        ({"rotary_dim": 130}, _ext.H3A_EINVAL, "even rotary dimension no wider than the head"),
+        ({"head_dim": 100, "rotary_dim": 96}, _ext.H3A_EUNSUPPORTED, "multiple of 8"),
+        ({"w_dtype": 5}, _ext.H3A_EINVAL, "weight dtype"),
+        ({"xk": 1 << 20}, _ext.H3A_EINVAL, "xk given without"),
+        ({"cos": None}, _ext.H3A_EINVAL, "cos/sin"),
+        ({"table_stride": 64}, _ext.H3A_EINVAL, "table_stride"),
+        ({"abi_version": 0}, _ext.H3A_EINVAL, "abi_version"),
+    ],
+)
+@host_only
+def test_rope_validation(lib, overrides, code, message):
+    a = _rope_args(**overrides)
+    assert lib.h3a_qknorm_rope(ctypes.byref(a), None) == code
+    assert message in _ext.last_error(lib)

@@ -1,0 +1,220 @@
+"""GPU parity of the HIP attention kernel against the CPU oracle.
+
+Tolerance (bf16 output against an fp32-accumulated SDPA-math reference on
+identical bf16 inputs): max abs <= 2e-2, mean abs <= 2e-3, |dLSE| <= 1e-3.
+Full-size workloads are checked on seeded samples of query rows (each row
+against the full key range) and through size-independent properties.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from h3_flash_amd import flash_attn_func, flash_attn_varlen_func
+from h3_flash_amd.prologue import fused_qk_norm_rope
+from h3_flash_amd.synth import WORKLOADS, make_raw
+from oracle.attention import sdpa_reference, sdpa_rows
+from oracle.metrics import ATTN_MAX_ABS, ATTN_MEAN_ABS, LSE_MAX_ABS, error_metrics
+from tests._golden import bf16, f32, golden
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _rand(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(shape, generator=g).to(torch.bfloat16)
+
+
+def assert_parity(out, lse, ref_out, ref_lse, tag=""):
+    m = error_metrics(out.float(), ref_out)
+    lse_err = (lse.detach().cpu().double() - ref_lse.double()).abs().max().item() if lse.numel() else 0.0
+    assert m["finite"], tag
+    assert m["max_abs"] <= ATTN_MAX_ABS, (tag, m)
+    assert m["mean_abs"] <= ATTN_MEAN_ABS, (tag, m)
+    assert lse_err <= LSE_MAX_ABS, (tag, lse_err)
+    return m, lse_err
+
+
+def run(q, k, v, **kw):
+    out, lse = flash_attn_func(q.to(DEV), k.to(DEV), v.to(DEV), **kw)
+    torch.cuda.synchronize()
+    return out.cpu(), lse.cpu()
+
+
+def test_golden_dense_cross_varlen():
+    g = golden()
+    scale = float(g["scale"])
+    for case in ("dense", "cross"):
+        out, lse = run(bf16(f"{case}_q"), bf16(f"{case}_k"), bf16(f"{case}_v"), softmax_scale=scale)
+        assert_parity(out, lse, f32(f"{case}_out"), f32(f"{case}_lse"), case)
+    cu = torch.from_numpy(g["varlen_cu"]).to(DEV)
+    out, lse = run(bf16("dense_q"), bf16("dense_k"), bf16("dense_v"), softmax_scale=scale, cu_seqlens_q=cu,
+                   cu_seqlens_k=cu, max_seqlen_q=47)
+    assert_parity(out, lse, f32("varlen_out"), f32("varlen_lse"), "varlen")
+
+
+@pytest.mark.parametrize(
+    "B,Sq,Sk,H",
+    [
+        (1, 1, 1, 1),
+        (1, 7, 7, 2),
+        (2, 63, 65, 3),
+        (1, 64, 64, 1),
+        (1, 65, 129, 2),
+        (1, 129, 1000, 1),
+        (1, 300, 300, 5),
+        (2, 1000, 513, 2),
+        (1, 2048, 77, 1),
+    ],
+)
+def test_ragged_shapes(B, Sq, Sk, H):
+    q, k, v = _rand((B, Sq, H, 128), 1), _rand((B, Sk, H, 128), 2), _rand((B, Sk, H, 128), 3)
+    out, lse = run(q, k, v)
+    ref_o, ref_l = sdpa_reference(q, k, v)
+    assert_parity(out, lse, ref_o, ref_l, (B, Sq, Sk, H))
+
+
+def test_c1_full():
+    w = WORKLOADS["c1"]
+    raw = make_raw(w)
+    out, lse = run(raw["q_raw"], raw["k_raw"], raw["v"])
+    ref_o, ref_l = sdpa_reference(raw["q_raw"], raw["k_raw"], raw["v"])
+    assert_parity(out, lse, ref_o, ref_l, "c1")
+
+
+def test_strided_views_of_packed_qkv():
+    # q/k/v as views of one (B, S, H, 3D) projection, like to_qkv(...).chunk(3)
+    qkv = _rand((2, 333, 3, 3 * 128), 4)
+    q, k, v = (t.to(DEV) for t in qkv.chunk(3, dim=-1))
+    assert not q.is_contiguous()
+    out, lse = flash_attn_func(q, k, v)
+    ref_o, ref_l = sdpa_reference(q.cpu(), k.cpu(), v.cpu())
+    assert_parity(out.cpu(), lse.cpu(), ref_o, ref_l, "strided")
+
+
+def test_softmax_scale_argument():
+    q, k, v = _rand((1, 200, 2, 128), 5), _rand((1, 300, 2, 128), 6), _rand((1, 300, 2, 128), 7)
+    for scale in (0.02, 0.25):
+        out, lse = run(q, k, v, softmax_scale=scale)
+        ref_o, ref_l = sdpa_reference(q, k, v, scale)
+        assert_parity(out, lse, ref_o, ref_l, scale)
+
+
+def test_preallocated_outputs_and_current_stream():
+    q, k, v = (_rand((1, 130, 1, 128), s).to(DEV) for s in (8, 9, 10))
+    out = torch.empty_like(q)
+    lse = torch.empty((1, 1, 130), dtype=torch.float32, device=DEV)
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        o2, l2 = flash_attn_func(q, k, v, out=out, lse=lse)
+    stream.synchronize()
+    assert o2.data_ptr() == out.data_ptr() and l2.data_ptr() == lse.data_ptr()
+    ref_o, ref_l = sdpa_reference(q.cpu(), k.cpu(), v.cpu())
+    assert_parity(out.cpu(), lse.cpu(), ref_o, ref_l, "stream")
+
+
+def test_varlen_many_segments_including_empty():
+    offs = [0, 1, 17, 17, 145, 146, 400, 657]
+    cu = torch.tensor(offs, dtype=torch.int32)
+    S = offs[-1]
+    q, k, v = _rand((1, S, 3, 128), 11), _rand((1, S, 3, 128), 12), _rand((1, S, 3, 128), 13)
+    out, lse = run(q, k, v, cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV))
+    ref_o, ref_l = sdpa_reference(q, k, v, cu_seqlens=cu)
+    assert_parity(out, lse, ref_o, ref_l, "varlen")
+    # FA varlen call form on (total, H, D)
+    o3, l3 = flash_attn_varlen_func(q[0].to(DEV), k[0].to(DEV), v[0].to(DEV), cu.to(DEV), cu.to(DEV), 256, 256)
+    assert torch.equal(o3.cpu(), out[0]) and torch.equal(l3.cpu(), lse[0])
+
+
+def test_empty_key_range_gives_zero_and_minus_inf():
+    q = _rand((1, 5, 1, 128), 14).to(DEV)
+    k = torch.empty((1, 0, 1, 128), dtype=torch.bfloat16, device=DEV)
+    out, lse = flash_attn_func(q, k, k)
+    torch.cuda.synchronize()
+    assert torch.all(out == 0) and torch.all(torch.isneginf(lse))
+
+
+def test_unsupported_requests_raise():
+    q = _rand((1, 8, 2, 128), 15).to(DEV)
+    with pytest.raises(RuntimeError, match="non-causal"):
+        flash_attn_func(q, q, q, causal=True)
+    with pytest.raises(RuntimeError, match="grouped-query"):
+        flash_attn_func(q, q[:, :, :1].contiguous(), q[:, :, :1].contiguous())
+    with pytest.raises(ValueError, match="head_dim"):
+        x = _rand((1, 8, 2, 64), 16).to(DEV)
+        flash_attn_func(x, x, x)
+
+
+def _prologue_inputs(name):
+    w = WORKLOADS[name]
+    raw = make_raw(w)
+    q, k = fused_qk_norm_rope(
+        raw["q_raw"].to(DEV), raw["k_raw"].to(DEV), raw["w_q"], raw["w_k"], raw["cos"], raw["sin"], raw["eps"], raw["eps"]
+    )
+    cu = raw["cu_seqlens"]
+    return q, k, raw["v"].to(DEV), cu
+
+
+def _sample_rows(S, n, seed, extra=()):
+    g = torch.Generator().manual_seed(seed)
+    rows = torch.randint(0, S, (n,), generator=g)
+    fixed = torch.tensor([0, 1, S - 1, S - 2, *extra], dtype=torch.int64)
+    return torch.unique(torch.cat((rows, fixed)))
+
+
+@pytest.mark.parametrize("name", ["c2", "c4"])
+def test_full_size_sampled_rows(name):
+    q, k, v, _ = _prologue_inputs(name)
+    out, lse = flash_attn_func(q, k, v)
+    torch.cuda.synchronize()
+    rows = _sample_rows(q.shape[1], 96, 17)
+    ref_o, ref_l = sdpa_rows(q.cpu(), k.cpu(), v.cpu(), rows)
+    assert_parity(out[:, rows.to(DEV)].cpu(), lse[:, :, rows.to(DEV)].cpu(), ref_o, ref_l, name)
+
+
+def test_c3_all_heads_sampled_rows():
+    q, k, v, _ = _prologue_inputs("c3")
+    out, lse = flash_attn_func(q, k, v)
+    torch.cuda.synchronize()
+    rows = _sample_rows(q.shape[1], 24, 18)
+    ref_o, ref_l = sdpa_rows(q.cpu(), k.cpu(), v.cpu(), rows)
+    assert_parity(out[:, rows.to(DEV)].cpu(), lse[:, :, rows.to(DEV)].cpu(), ref_o, ref_l, "c3")
+
+
+def test_c5_packed_varlen_sampled_rows():
+    q, k, v, cu = _prologue_inputs("c5")
+    out, lse = flash_attn_func(q, k, v, cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV), max_seqlen_q=49920)
+    torch.cuda.synchronize()
+    # rows from both segments, including the ragged audio tail 51,200 .. 51,215
+    rows = _sample_rows(q.shape[1], 96, 19, extra=(49919, 49920, 49921, 51199, 51200, 51207, 51215))
+    ref_o, ref_l = sdpa_rows(q.cpu(), k.cpu(), v.cpu(), rows, cu_seqlens=cu)
+    assert_parity(out[:, rows.to(DEV)].cpu(), lse[:, :, rows.to(DEV)].cpu(), ref_o, ref_l, "c5")
+    # the audio segment must not see video keys: compare with a standalone run
+    a0 = 49920
+    oa_, la_ = flash_attn_func(q[:, a0:].contiguous(), k[:, a0:].contiguous(), v[:, a0:].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(oa_, out[:, a0:]) and torch.equal(la_, lse[:, :, a0:])
+
+
+def test_c2_full_size_properties():
+    q, k, v, _ = _prologue_inputs("c2")
+    out, lse = flash_attn_func(q, k, v)
+    # (1) rows are convex combinations of v rows: bounded by the column extrema
+    vmin, vmax = v.float().amin(dim=1, keepdim=True), v.float().amax(dim=1, keepdim=True)
+    assert torch.all(out.float() >= vmin - 1e-2) and torch.all(out.float() <= vmax + 1e-2)
+    # (2) constant values are reproduced whatever the weights
+    ones = torch.ones_like(v)
+    o1, l1 = flash_attn_func(q, k, ones)
+    assert (o1.float() - 1.0).abs().max().item() <= 8e-3
+    assert torch.equal(l1, lse)  # LSE does not depend on v
+    # (3) a joint permutation of keys and values leaves the output unchanged
+    perm = torch.randperm(k.shape[1], generator=torch.Generator().manual_seed(3)).to(DEV)
+    o2, l2 = flash_attn_func(q, k[:, perm].contiguous(), v[:, perm].contiguous())
+    assert (o2.float() - out.float()).abs().max().item() <= 2e-2
+    assert (l2 - lse).abs().max().item() <= 1e-3
+    # (4) deterministic: same inputs, same bits
+    o3, l3 = flash_attn_func(q, k, v)
+    assert torch.equal(o3, out) and torch.equal(l3, lse)
+    torch.cuda.synchronize()
