@@ -42,10 +42,30 @@ def parse_args(argv=None):
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
-    p.add_argument("--cpu-rows", type=int, default=4096, help="query rows in the CPU baseline sample")
-    p.add_argument("--cpu-repeats", type=int, default=3)
+    p.add_argument("--cpu-rows", type=int, default=0, help="query rows in the CPU baseline sample (0: all)")
+    p.add_argument("--cpu-repeats", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument(
+        "--copy-calibration",
+        type=int,
+        default=0,
+        metavar="MIB",
+        help="only run 5 device-to-device copies of MIB MiB (scales rocprofv3 FETCH_SIZE/WRITE_SIZE)",
+    )
     return p.parse_args(argv)
+
+
+def copy_calibration(torch, mib: int) -> int:
+    """Plain device copies of a known size, for calibrating HBM byte counters."""
+
+    n = mib * (1 << 20)
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n, "copy_calibration_bytes_written": n, "copies": 5}))
+    return 0
 
 
 def cpu_model() -> str:
@@ -66,20 +86,20 @@ def cpu_baseline(torch, q, k, v, heads, rows: int, repeats: int) -> dict:
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    rows = min(rows, q.shape[1])
-    qs = q[:, :rows].cpu()
+    rows = q.shape[1] if rows <= 0 else min(rows, q.shape[1])
     kc, vc = k.cpu(), v.cpu()
 
-    def call():
+    def call(n):
+        qs = q[:, :n].cpu()
         return functional.scaled_dot_product_attention(
             qs.transpose(1, 2), kc.transpose(1, 2), vc.transpose(1, 2), dropout_p=0.0, is_causal=False
         ).transpose(1, 2)
 
-    call()  # warm-up outside the samples
+    call(min(rows, 512))  # warm-up outside the samples
     samples = []
     for _ in range(repeats):
         t0 = time.perf_counter()
-        call()
+        call(rows)
         samples.append(time.perf_counter() - t0)
     med = statistics.median(samples)
     flops = 4.0 * rows * kc.shape[1] * q.shape[-1] * heads
@@ -89,10 +109,10 @@ def cpu_baseline(torch, q, k, v, heads, rows: int, repeats: int) -> dict:
         "cores": torch.get_num_threads(),
         "kind": "reference",
         "sample": (
-            f"torch {torch.__version__} F.scaled_dot_product_attention on CPU bf16, first {rows} query rows x "
-            f"{kc.shape[1]} keys x {heads} heads (4*rows*S*D*H = {flops:.3e} flop), median of {repeats} "
-            f"after 1 warm-up ({', '.join(f'{s:.2f}' for s in samples)} s); host {cpu_model()}, "
-            f"{cores} cores in affinity"
+            f"torch {torch.__version__} F.scaled_dot_product_attention on CPU bf16 (BHSD transposes of the "
+            f"BSHD workload tensors), first {rows} query rows x {kc.shape[1]} keys x {heads} heads "
+            f"(4*rows*S*D*H = {flops:.3e} flop), median of {repeats} after a 512-row warm-up "
+            f"({', '.join(f'{s:.2f}' for s in samples)} s); host {cpu_model()}, {cores} cores in affinity"
         ),
     }
 
@@ -131,6 +151,8 @@ def main(argv=None) -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
+    if args.copy_calibration:
+        return copy_calibration(torch, args.copy_calibration)
     dev = torch.device("cuda:0")
     w = WORKLOADS[args.workload]
     raw = make_raw(w)

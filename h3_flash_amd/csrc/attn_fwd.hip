@@ -9,15 +9,21 @@
 //     S^T = K Q^T (v_mfma_f32_32x32x16_bf16). Computing S transposed puts one
 //     query column per lane, so the row max / row sum of the online softmax
 //     are in-lane reductions plus one v_permlane32_swap across wave halves;
-//   * K/V tiles of 64 keys are double-buffered through LDS: tile j+1 is read
-//     from HBM (128-bit buffer loads) into VGPRs while tile j is consumed,
-//     then written to the other LDS stage behind one barrier per tile;
-//   * V is transposed while it is staged (V^T rows of 64 keys) so that the
-//     PV product O^T = V^T P^T takes its A operand with 64-bit LDS reads and
-//     its B operand (P^T, bf16) straight from the S^T accumulators;
+//   * K and V tiles of 64 keys are staged key-major in LDS, double-buffered:
+//     while tile j is consumed, tiles j+1 (V) / j+2 (K) are read from HBM with
+//     128-bit buffer loads into VGPRs and written behind one barrier per tile;
+//   * the PV product O^T = V^T P^T takes its A operand with the gfx950
+//     transpose read ds_read_b64_tr_b16 (four keys of one head-dim column per
+//     lane) and its B operand (P^T, bf16) straight from the S^T accumulators;
+//   * software pipeline: iteration j issues the QK^T MFMAs of tile j+1, then
+//     the PV MFMAs of tile j, and the softmax VALU work of tile j+1 (which only
+//     depends on the first group) overlaps the second group;
 //   * softmax runs in the exp2 domain with fp32 running max / sum; the running
 //     max is only raised when a tile exceeds it by more than 2^8, so the O
 //     rescale is skipped for almost every tile.
+// LDS row strides are padded so that every access pattern is bank-conflict
+// free: K rows (272 B) shift 4 banks per row for the 16-lane b128 reads; V rows
+// (320 B) shift 16 banks per row for the 4-row x 32-byte transpose reads.
 #include "common.h"
 #include "kernels.h"
 
@@ -29,22 +35,33 @@ constexpr int kBM = 128;          // query rows per workgroup
 constexpr int kBN = 64;           // keys per tile
 constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
-constexpr int kKRow = kD * 2 + 16;    // LDS bytes per K row (pad: 4 banks)
-constexpr int kVRow = kBN * 2 + 8;    // LDS bytes per V^T row
+constexpr int kKRow = kD * 2 + 16;    // LDS bytes per K row
+constexpr int kVRow = kD * 2 + 64;    // LDS bytes per V row
 constexpr int kKBytes = kBN * kKRow;  // 17408
-constexpr int kVBytes = kD * kVRow;   // 17408
-constexpr int kStage = kKBytes + kVBytes;
-constexpr int kLdsBytes = 2 * kStage;
+constexpr int kVBytes = kBN * kVRow;  // 20480
+constexpr int kLdsBytes = 2 * (kKBytes + kVBytes);
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
 
 static_assert(kThreads == 256, "staging maps assume 256 threads");
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 __device__ __forceinline__ uint32_t span_bytes(int rows, int row_bytes) {
     return rows > 0 ? (uint32_t)((rows - 1) * row_bytes + kD * 2) : 0u;
 }
 
+// Four bf16 of one head-dim column: within each 16-lane group lane i receives
+// element (i & 3) of the 8-byte chunks addressed by lanes 4j + (i >> 2).
+__device__ __forceinline__ i32x2 read_tr(const char* p) {
+    s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+    return __builtin_bit_cast(i32x2, v);
+}
+
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
+    char* const kst = smem;                // K stages 0, 1
+    char* const vst = smem + 2 * kKBytes;  // V stages 0, 1
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -93,34 +110,46 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         qf[ks] = __builtin_bit_cast(bf16x8, raw);
     }
 
-    // Staging maps. K: thread owns rows (tid>>4) + 16*i, 16-byte chunk tid&15.
-    // V: thread owns keys 4*(tid>>4) .. +3, head dims 8*(tid&15) .. +7.
+    // Staging map (K and V alike): thread owns rows (tid>>4) + 16*i of a tile
+    // and their 16-byte chunk tid&15; 16 lanes cover one 256-byte row.
     const int st_row = tid >> 4;
     const int st_chk = tid & 15;
     i32x4 kreg[4], vreg[4];
-
-    auto load_tile = [&](int n0) {
+    auto load_k = [&](int tile) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            kreg[i] = buf_load16(rk, (uint32_t)((n0 + st_row + 16 * i) * p.k_rs + st_chk * 16));
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-            vreg[r] = buf_load16(rv, (uint32_t)((n0 + 4 * st_row + r) * p.v_rs + st_chk * 16));
+            kreg[i] = buf_load16(rk, (uint32_t)((tile * kBN + st_row + 16 * i) * p.k_rs + st_chk * 16));
     };
-    auto store_tile = [&](int stage) {
-        char* kl = smem + stage * kStage;
-        char* vl = kl + kKBytes;
+    auto load_v = [&](int tile) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            *(i32x4*)(kl + (st_row + 16 * i) * kKRow + st_chk * 16) = kreg[i];
+            vreg[i] = buf_load16(rv, (uint32_t)((tile * kBN + st_row + 16 * i) * p.v_rs + st_chk * 16));
+    };
+    auto store_k = [&](int stage) {
+        char* dst = kst + stage * kKBytes + st_row * kKRow + st_chk * 16;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int dw = e >> 1;
-            const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-            i32x2 pr;
-            pr.x = (int)__builtin_amdgcn_perm((uint32_t)vreg[1][dw], (uint32_t)vreg[0][dw], sel);
-            pr.y = (int)__builtin_amdgcn_perm((uint32_t)vreg[3][dw], (uint32_t)vreg[2][dw], sel);
-            *(i32x2*)(vl + (st_chk * 8 + e) * kVRow + st_row * 8) = pr;
+        for (int i = 0; i < 4; ++i) *(i32x4*)(dst + 16 * i * kKRow) = kreg[i];
+    };
+    auto store_v = [&](int stage) {
+        char* dst = vst + stage * kVBytes + st_row * kVRow + st_chk * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) *(i32x4*)(dst + 16 * i * kVRow) = vreg[i];
+    };
+
+    const float c = p.scale_log2;
+    const int ntiles = (sk + kBN - 1) / kBN;
+
+    // S^T (64 keys x 32 queries) = K_tile Q^T from K stage `stage`.
+    auto qk = [&](int stage, f32x16* s) {
+        const char* kl = kst + stage * kKBytes + l32 * kKRow + hi * 16;
+#pragma unroll
+        for (int nb2 = 0; nb2 < 2; ++nb2) {
+            s[nb2] = f32x16{};
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                bf16x8 a = *(const bf16x8*)(kl + nb2 * 32 * kKRow + ks * 32);
+                s[nb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[nb2], 0, 0, 0);
+            }
         }
     };
 
@@ -129,36 +158,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     for (int db = 0; db < 4; ++db) oacc[db] = f32x16{};
     float m_run = -INFINITY;  // running max of raw scores for this lane's query
     float l_run = 0.f;        // this lane's partial sum (its half of the keys)
-    const float c = p.scale_log2;
+    bf16x8 pf[4];             // P^T of the tile waiting for its PV product
 
-    const int ntiles = (sk + kBN - 1) / kBN;
-    if (ntiles > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
-    __syncthreads();
-
-    for (int j = 0; j < ntiles; ++j) {
-        const int n0 = j * kBN;
-        const bool more = j + 1 < ntiles;
-        if (more) load_tile(n0 + kBN);
-
-        const char* kl = smem + (j & 1) * kStage;
-        const char* vl = kl + kKBytes;
-
-        // S^T (64 keys x 32 queries) = K_tile Q^T
-        f32x16 s[2];
-#pragma unroll
-        for (int nb2 = 0; nb2 < 2; ++nb2) {
-            s[nb2] = f32x16{};
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                bf16x8 a = *(const bf16x8*)(kl + (nb2 * 32 + l32) * kKRow + ks * 32 + hi * 16);
-                s[nb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[nb2], 0, 0, 0);
-            }
-        }
-        // Keys past the end of the sequence (ragged last tile) get -inf.
-        if (n0 + kBN > sk) {
+    // Online softmax of tile `tile` held in s: updates m_run / l_run and
+    // writes the bf16 P^T fragments; returns the factor alpha by which the
+    // accumulated O must be rescaled (exactly 1 unless the running max rose
+    // by more than the threshold). Branch-free, so the scheduler can overlap
+    // it with the PV MFMAs issued before it.
+    auto softmax = [&](f32x16* s, int tile, bool ragged) -> float {
+        if (ragged) {  // last tile: keys past the end get -inf
+            const int n0 = tile * kBN;
 #pragma unroll
             for (int nb2 = 0; nb2 < 2; ++nb2)
 #pragma unroll
@@ -167,71 +176,131 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
                     if (key >= sk) s[nb2][r] = -INFINITY;
                 }
         }
-
-        // Online softmax (exp2 domain).
-        float mx = s[0][0];
+        float mx = fmaxf(s[0][0], s[1][0]);
 #pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[0][r]);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[1][r]);
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
         {
             f32x2 pr = halves(mx);
             mx = fmaxf(pr.x, pr.y);
         }
         const float m_new = fmaxf(m_run, mx);
-        const bool need = (m_new - m_run) * c > kRescaleThreshold;
-        if (__builtin_amdgcn_ballot_w64(need)) {
-            const float m_use = need ? m_new : m_run;
-            const float alpha = fast_exp2((m_run - m_use) * c);
-            m_run = m_use;
-            l_run *= alpha;
+        const float m_use = (m_new - m_run) * c > kRescaleThreshold ? m_new : m_run;
+        const float alpha = fast_exp2((m_run - m_use) * c);
+        m_run = m_use;
+        const float mc = m_use * c;
+        float lsum = 0.f;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            // k-step cc covers keys 16*cc .. +15: accumulator registers
+            // 8*(cc&1) .. +7 of s[cc>>1]
+            f32x8 t;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float pv = fast_exp2(__builtin_fmaf(s[cc >> 1][(cc & 1) * 8 + i], c, -mc));
+                t[i] = pv;
+                lsum += pv;
+            }
+            pf[cc] = __builtin_convertvector(t, bf16x8);
+        }
+        l_run = __builtin_fmaf(l_run, alpha, lsum);
+        return alpha;
+    };
+    // Keep the exp/convert work in its block, next to the PV MFMAs it
+    // overlaps, instead of letting it sink past the rescale branch. (An empty
+    // volatile asm also closes the scheduling region.)
+    auto pin_softmax = [&]() {
+        asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(pf[2]), "v"(pf[3]), "v"(l_run));
+    };
+    auto rescale = [&](float alpha) {
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
             for (int db = 0; db < 4; ++db)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
         }
-        const float mc = m_run * c;
-        float lsum = 0.f;
-#pragma unroll
-        for (int nb2 = 0; nb2 < 2; ++nb2)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float pv = fast_exp2(__builtin_fmaf(s[nb2][r], c, -mc));
-                s[nb2][r] = pv;
-                lsum += pv;
-            }
-        l_run += lsum;
+    };
 
-        // P^T fragments: k-step cc covers keys 16*cc .. +15 and is made of
-        // accumulator registers 8*(cc&1) .. +7 of s[cc>>1].
-        bf16x8 pf[4];
+    // O^T (128 dims x 32 queries) += V^T P^T from V stage `stage`.
+    auto pv = [&](int stage) {
+        // transpose-read addresses: lane (l & 15) of a 16-lane group reads key
+        // row (l & 15) >> 2 and dims 4*(l & 3) .. +3 of its group's 16 columns
+        const int g = lane & 15;
+        const char* vl = vst + stage * kVBytes + ((g >> 2) + hi * 4) * kVRow + (((lane >> 4) & 1) * 16 + 4 * (g & 3)) * 2;
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-            const int nb2 = cc >> 1, rb = (cc & 1) * 8;
-            f32x8 t;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) t[i] = s[nb2][rb + i];
-            pf[cc] = __builtin_convertvector(t, bf16x8);
-        }
-
-        // O^T (128 dims x 32 queries) += V^T P^T
-#pragma unroll
-        for (int db = 0; db < 4; ++db) {
-            const char* vrow = vl + (db * 32 + l32) * kVRow;
+        for (int db = 0; db < 4; ++db)
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc) {
-                const int key = cc * 16 + hi * 4;
-                i32x2 lo = *(const i32x2*)(vrow + key * 2);
-                i32x2 hi2 = *(const i32x2*)(vrow + (key + 8) * 2);
-                i32x4 av = {lo.x, lo.y, hi2.x, hi2.y};
-                oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av), pf[cc],
-                                                                  oacc[db], 0, 0, 0);
+                const char* a0 = vl + (cc * 16) * kVRow + db * 64;
+                i32x2 lo = read_tr(a0);
+                i32x2 up = read_tr(a0 + 8 * kVRow);
+                i32x4 av = {lo.x, lo.y, up.x, up.y};
+                oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av), pf[cc], oacc[db],
+                                                                  0, 0, 0);
             }
-        }
+    };
 
-        if (more) store_tile((j + 1) & 1);
+    // Pipeline: before iteration j, P_j is in registers, K_{j+1} and V_j are
+    // in LDS. Iteration j computes S_{j+1} and O += V_j P_j, then the softmax
+    // of S_{j+1}, while K_{j+2} and V_{j+1} travel HBM -> VGPR -> LDS.
+    const bool ragged = ntiles * kBN > sk;
+    if (ntiles > 0) {
+        load_k(0);
+        load_v(0);
+        store_k(0);
+        store_v(0);
+        if (ntiles > 1) {
+            load_k(1);
+            store_k(1);
+        }
+        __syncthreads();
+        f32x16 s[2];
+        qk(0, s);
+        softmax(s, 0, ntiles == 1 && ragged);
+        __syncthreads();  // K stage 0 is refilled in the first iteration
+    }
+    int j = 0;
+    for (; j + 2 < ntiles; ++j) {  // steady state: tiles j+1 and j+2 exist
+        load_k(j + 2);
+        load_v(j + 1);
+        f32x16 s[2];
+        qk((j + 1) & 1, s);
+        pv(j & 1);
+        const float alpha = softmax(s, j + 1, false);
+        // Issue order for the block above: the HBM loads, then each QK^T MFMA
+        // behind its K fragment read, then each PV MFMA behind its two
+        // transpose reads followed by a slice of the softmax VALU work, so the
+        // softmax issues while the PV MFMAs execute.
+        __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);  // VMEM read
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // VALU
+        }
+        pin_softmax();
+        rescale(alpha);
+        store_k(j & 1);
+        store_v((j + 1) & 1);
         __syncthreads();
     }
+    if (j + 1 < ntiles) {  // j = ntiles - 2: the last tile is loaded, no K beyond
+        load_v(j + 1);
+        f32x16 s[2];
+        qk((j + 1) & 1, s);
+        pv(j & 1);
+        const float alpha = softmax(s, j + 1, ragged);
+        pin_softmax();
+        rescale(alpha);
+        store_v((j + 1) & 1);
+        __syncthreads();
+        ++j;
+    }
+    if (j < ntiles) pv(j & 1);  // j = ntiles - 1
 
     // Epilogue: combine the two halves' partial sums, normalise, store.
     {

@@ -86,8 +86,8 @@ def test_c1_full():
 
 def test_strided_views_of_packed_qkv():
     # q/k/v as views of one (B, S, H, 3D) projection, like to_qkv(...).chunk(3)
-    qkv = _rand((2, 333, 3, 3 * 128), 4)
-    q, k, v = (t.to(DEV) for t in qkv.chunk(3, dim=-1))
+    qkv = _rand((2, 333, 3, 3 * 128), 4).to(DEV)
+    q, k, v = qkv.chunk(3, dim=-1)
     assert not q.is_contiguous()
     out, lse = flash_attn_func(q, k, v)
     ref_o, ref_l = sdpa_reference(q.cpu(), k.cpu(), v.cpu())

@@ -1,9 +1,12 @@
 """GPU parity of the fused q/k RMSNorm + RoPE kernel against the fp32 oracle.
 
 Both compute in fp32 and round once to bf16, so the bar is: every element
-within one bf16 ulp of the oracle's bf16 result and at least 99.9% of
-elements bit-identical (summation order of the row norm and FMA contraction
-may move a value across a rounding boundary).
+within one bf16 ulp of the oracle's bf16 result (or within 2e-6 absolute,
+the fp32 cancellation error of n*cos - n'*sin for |n| up to ~8, where the
+result is far below bf16 resolution at unit scale) and at least 99.9% of
+elements bit-identical. Summation order of the row norm and FMA contraction
+move an fp32 value by about one fp32 ulp, which flips the bf16 rounding only
+for values within that distance of a rounding midpoint.
 """
 
 from __future__ import annotations
@@ -30,7 +33,8 @@ def assert_rounding_parity(actual: torch.Tensor, expect_bf16: torch.Tensor, tag=
     a = actual.detach().cpu().float()
     e = expect_bf16.detach().cpu().float()
     diff = (a - e).abs()
-    assert torch.all(diff <= bf16_ulp(e) * 1.0001), (tag, diff.max().item())
+    bound = torch.maximum(bf16_ulp(e) * 1.0001, torch.full_like(e, 2e-6))
+    assert torch.all(diff <= bound), (tag, (diff / bound).max().item())
     exact = (diff == 0).float().mean().item()
     assert exact >= 0.999, (tag, exact)
 
