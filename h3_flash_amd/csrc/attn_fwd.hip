@@ -4,52 +4,62 @@
 // O = softmax(scale * Q K^T) V over the full key range of each (batch, head),
 // or of each packed segment when cu_seqlens are given.
 //
-// Tiling (one workgroup = 4 waves = 128 query rows of one head):
+// Tiling: one workgroup = 8 waves = 256 query rows of one head, one workgroup
+// per CU (two waves per SIMD).
 //   * each wave keeps 32 query rows resident in VGPRs as the B operand of
 //     S^T = K Q^T (v_mfma_f32_32x32x16_bf16). Computing S transposed puts one
 //     query column per lane, so the row max / row sum of the online softmax
 //     are in-lane reductions plus one v_permlane32_swap across wave halves;
-//   * K and V tiles of 64 keys are staged key-major in LDS, double-buffered:
-//     while tile j is consumed, tiles j+1 (V) / j+2 (K) are read from HBM with
-//     128-bit buffer loads into VGPRs and written behind one barrier per tile;
+//   * K and V tiles of 64 keys go HBM -> LDS directly (buffer_load ... lds,
+//     16 bytes per lane, no VGPR staging) into three LDS stages each, issued
+//     two tiles ahead of use, so a full iteration hides the load latency;
+//     one barrier per tile, after each wave's own loads of the previous
+//     iteration are complete (s_waitcnt vmcnt);
 //   * the PV product O^T = V^T P^T takes its A operand with the gfx950
 //     transpose read ds_read_b64_tr_b16 (four keys of one head-dim column per
 //     lane) and its B operand (P^T, bf16) straight from the S^T accumulators;
-//   * software pipeline: iteration j issues the QK^T MFMAs of tile j+1, then
-//     the PV MFMAs of tile j, and the softmax VALU work of tile j+1 (which only
-//     depends on the first group) overlaps the second group;
+//   * software pipeline (hand scheduled, sched_barrier fenced): iteration j
+//     issues the 16 QK^T MFMAs of tile j+1 with their K fragments read four
+//     MFMAs ahead, then the 16 PV MFMAs of tile j, each followed by its
+//     transpose reads four MFMAs ahead and a slice of the softmax of tile j+1;
 //   * softmax runs in the exp2 domain with fp32 running max / sum; the running
 //     max is only raised when a tile exceeds it by more than 2^8, so the O
 //     rescale is skipped for almost every tile.
-// LDS row strides are padded so that every access pattern is bank-conflict
-// free: K rows (272 B) shift 4 banks per row for the 16-lane b128 reads; V rows
-// (320 B) shift 16 banks per row for the 4-row x 32-byte transpose reads.
+// LDS rows are 256 bytes, unpadded; the 16-byte chunk c of row r is stored at
+// chunk c ^ swz(r), swz(r) = 4*(r & 3) + ((r >> 2) & 3). Both read patterns are
+// then bank-conflict free: the K reads (16 consecutive rows, one chunk) and the
+// V transpose reads (4 consecutive rows x 4 chunks per 32 lanes).
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
 namespace h3a {
 namespace {
 
-constexpr int kD = 128;           // head dim
-constexpr int kBM = 128;          // query rows per workgroup
-constexpr int kBN = 64;           // keys per tile
-constexpr int kWaves = 4;
+constexpr int kD = 128;            // head dim
+constexpr int kBM = 256;           // query rows per workgroup
+constexpr int kBN = 64;            // keys per tile
+constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
-constexpr int kKRow = kD * 2 + 16;    // LDS bytes per K row
-constexpr int kVRow = kD * 2 + 64;    // LDS bytes per V row
-constexpr int kKBytes = kBN * kKRow;  // 17408
-constexpr int kVBytes = kBN * kVRow;  // 20480
-constexpr int kLdsBytes = 2 * (kKBytes + kVBytes);
-constexpr float kRescaleThreshold = 8.0f;  // log2 units
+constexpr int kStages = 3;
+constexpr int kRow = kD * 2;       // LDS bytes per K / V row
+constexpr int kTile = kBN * kRow;  // 16384
+constexpr int kLdsBytes = 2 * kStages * kTile;
+constexpr int kDmaPerTile = kBN / (kWaves * 4);  // 4-row DMA loads per wave per tile
+constexpr float kRescaleThreshold = 8.0f;        // log2 units
 
-static_assert(kThreads == 256, "staging maps assume 256 threads");
+static_assert(kDmaPerTile == 2, "vmcnt accounting below assumes 2 K + 2 V loads per iteration");
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ uint32_t span_bytes(int rows, int row_bytes) {
     return rows > 0 ? (uint32_t)((rows - 1) * row_bytes + kD * 2) : 0u;
 }
+
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 // Four bf16 of one head-dim column: within each 16-lane group lane i receives
 // element (i & 3) of the 8-byte chunks addressed by lanes 4j + (i >> 2).
@@ -58,15 +68,26 @@ __device__ __forceinline__ i32x2 read_tr(const char* p) {
     return __builtin_bit_cast(i32x2, v);
 }
 
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier that leaves the memory counters to the caller: the LDS
+// DMA loads in flight are waited for explicitly (wait_vmcnt) before it.
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
-    __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
-    char* const kst = smem;                // K stages 0, 1
-    char* const vst = smem + 2 * kKBytes;  // V stages 0, 1
+    __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+    char* const kst = smem;                    // K stages 0..2
+    char* const vst = smem + kStages * kTile;  // V stages 0..2
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int hi = lane >> 5;   // wave half
+    const int hi = lane >> 5;  // wave half
     const int l32 = lane & 31;
 
     // Workgroups are dispatched round-robin over the 8 XCDs. Renumber them so
@@ -110,48 +131,46 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         qf[ks] = __builtin_bit_cast(bf16x8, raw);
     }
 
-    // Staging map (K and V alike): thread owns rows (tid>>4) + 16*i of a tile
-    // and their 16-byte chunk tid&15; 16 lanes cover one 256-byte row.
-    const int st_row = tid >> 4;
-    const int st_chk = tid & 15;
-    i32x4 kreg[4], vreg[4];
-    auto load_k = [&](int tile) {
+    // DMA map: wave w fills rows 8w .. 8w+7 of a tile with two 4-row loads;
+    // lane L writes LDS chunk (L & 15) of row r0 + (L >> 4), which holds the
+    // tile's chunk (L & 15) ^ swz(row) of that key row.
+    int dma_off[kDmaPerTile];
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            kreg[i] = buf_load16(rk, (uint32_t)((tile * kBN + st_row + 16 * i) * p.k_rs + st_chk * 16));
-    };
-    auto load_v = [&](int tile) {
+    for (int i = 0; i < kDmaPerTile; ++i) {
+        const int r = (wave * kDmaPerTile + i) * 4 + (lane >> 4);
+        dma_off[i] = ((lane & 15) ^ swz(r)) << 4;
+    }
+    auto dma = [&](__amdgpu_buffer_rsrc_t rsrc, int row_bytes, char* stage, int tile) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            vreg[i] = buf_load16(rv, (uint32_t)((tile * kBN + st_row + 16 * i) * p.v_rs + st_chk * 16));
+        for (int i = 0; i < kDmaPerTile; ++i) {
+            const int r0 = (wave * kDmaPerTile + i) * 4;
+            const uint32_t voff = (uint32_t)((tile * kBN + r0 + (lane >> 4)) * row_bytes + dma_off[i]);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(stage + r0 * kRow), 16, voff, 0, 0, 0);
+        }
     };
-    auto store_k = [&](int stage) {
-        char* dst = kst + stage * kKBytes + st_row * kKRow + st_chk * 16;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) *(i32x4*)(dst + 16 * i * kKRow) = kreg[i];
-    };
-    auto store_v = [&](int stage) {
-        char* dst = vst + stage * kVBytes + st_row * kVRow + st_chk * 16;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) *(i32x4*)(dst + 16 * i * kVRow) = vreg[i];
-    };
+    auto dma_k = [&](int tile) { dma(rk, p.k_rs, kst + (tile % kStages) * kTile, tile); };
+    auto dma_v = [&](int tile) { dma(rv, p.v_rs, vst + (tile % kStages) * kTile, tile); };
+
+    // K fragment of QK^T MFMA t (key block t & 1, head-dim step t >> 1): row
+    // 32*(t & 1) + l32, logical chunk 2*(t >> 1) + hi.
+    // The swizzle only moves bits 4-7 of an in-row byte offset, so every
+    // fragment address is a per-lane base XOR a per-step constant. K: offset
+    // kbase ^ (32*ks) (+32 rows for the second key block).
+    const int kbase = l32 * kRow + ((hi ^ swz(l32)) << 4);
+    // Transpose-read addresses of PV MFMA t (head-dim block db = t >> 2, key
+    // step cc = t & 3): lane (g = l & 15) of a 16-lane group reads row
+    // 16*cc + 4*hi + (g >> 2) (+8 for the upper four keys) and head dims
+    // 32*db + 16*((l >> 4) & 1) + 4*(g & 3) .. +3. With swz(row) =
+    // 4*(g >> 2) ^ hi ^ 2*upper, the offset is
+    // 4096*cc + 2048*upper + (vbase ^ 64*db ^ 32*upper).
+    int vbase;
+    {
+        const int g = lane & 15, jr = g >> 2, dgrp = (lane >> 4) & 1, u = (g & 3) >> 1;
+        vbase = (4 * hi + jr) * kRow + ((32 * dgrp) ^ (16 * u) ^ (64 * jr) ^ (16 * hi)) + (g & 1) * 8;
+    }
 
     const float c = p.scale_log2;
     const int ntiles = (sk + kBN - 1) / kBN;
-
-    // S^T (64 keys x 32 queries) = K_tile Q^T from K stage `stage`.
-    auto qk = [&](int stage, f32x16* s) {
-        const char* kl = kst + stage * kKBytes + l32 * kKRow + hi * 16;
-#pragma unroll
-        for (int nb2 = 0; nb2 < 2; ++nb2) {
-            s[nb2] = f32x16{};
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks) {
-                bf16x8 a = *(const bf16x8*)(kl + nb2 * 32 * kKRow + ks * 32);
-                s[nb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ks], s[nb2], 0, 0, 0);
-            }
-        }
-    };
 
     f32x16 oacc[4];
 #pragma unroll
@@ -160,56 +179,24 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     float l_run = 0.f;        // this lane's partial sum (its half of the keys)
     bf16x8 pf[4];             // P^T of the tile waiting for its PV product
 
-    // Online softmax of tile `tile` held in s: updates m_run / l_run and
-    // writes the bf16 P^T fragments; returns the factor alpha by which the
-    // accumulated O must be rescaled (exactly 1 unless the running max rose
-    // by more than the threshold). Branch-free, so the scheduler can overlap
-    // it with the PV MFMAs issued before it.
-    auto softmax = [&](f32x16* s, int tile, bool ragged) -> float {
-        if (ragged) {  // last tile: keys past the end get -inf
-            const int n0 = tile * kBN;
-#pragma unroll
-            for (int nb2 = 0; nb2 < 2; ++nb2)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = n0 + nb2 * 32 + (r >> 2) * 8 + hi * 4 + (r & 3);
-                    if (key >= sk) s[nb2][r] = -INFINITY;
-                }
-        }
-        float mx = fmaxf(s[0][0], s[1][0]);
-#pragma unroll
-        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
-        {
-            f32x2 pr = halves(mx);
-            mx = fmaxf(pr.x, pr.y);
-        }
-        const float m_new = fmaxf(m_run, mx);
-        const float m_use = (m_new - m_run) * c > kRescaleThreshold ? m_new : m_run;
-        const float alpha = fast_exp2((m_run - m_use) * c);
-        m_run = m_use;
-        const float mc = m_use * c;
-        float lsum = 0.f;
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-            // k-step cc covers keys 16*cc .. +15: accumulator registers
-            // 8*(cc&1) .. +7 of s[cc>>1]
-            f32x8 t;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float pv = fast_exp2(__builtin_fmaf(s[cc >> 1][(cc & 1) * 8 + i], c, -mc));
-                t[i] = pv;
-                lsum += pv;
-            }
-            pf[cc] = __builtin_convertvector(t, bf16x8);
-        }
-        l_run = __builtin_fmaf(l_run, alpha, lsum);
-        return alpha;
+    auto kread = [&](const char* kl, int t) {
+        return *(const bf16x8*)(kl + (t & 1) * 32 * kRow + (kbase ^ (32 * (t >> 1))));
     };
-    // Keep the exp/convert work in its block, next to the PV MFMAs it
-    // overlaps, instead of letting it sink past the rescale branch. (An empty
-    // volatile asm also closes the scheduling region.)
-    auto pin_softmax = [&]() {
-        asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(pf[2]), "v"(pf[3]), "v"(l_run));
+    auto vread = [&](const char* vl, int t) {
+        const char* a = vl + (t & 3) * 16 * kRow;
+        const int x = vbase ^ (64 * (t >> 2));
+        const i32x2 lo = read_tr(a + x);
+        const i32x2 up = read_tr(a + 8 * kRow + (x ^ 32));
+        return __builtin_bit_cast(bf16x8, i32x4{lo.x, lo.y, up.x, up.y});
+    };
+    auto mask_tail = [&](f32x16& s0, f32x16& s1, int tile) {
+        const int n0 = tile * kBN;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = n0 + (r >> 2) * 8 + hi * 4 + (r & 3);
+            if (key >= sk) s0[r] = -INFINITY;
+            if (key + 32 >= sk) s1[r] = -INFINITY;
+        }
     };
     auto rescale = [&](float alpha) {
         if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
@@ -219,88 +206,117 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
                 for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
         }
     };
-
-    // O^T (128 dims x 32 queries) += V^T P^T from V stage `stage`.
-    auto pv = [&](int stage) {
-        // transpose-read addresses: lane (l & 15) of a 16-lane group reads key
-        // row (l & 15) >> 2 and dims 4*(l & 3) .. +3 of its group's 16 columns
-        const int g = lane & 15;
-        const char* vl = vst + stage * kVBytes + ((g >> 2) + hi * 4) * kVRow + (((lane >> 4) & 1) * 16 + 4 * (g & 3)) * 2;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int cc = 0; cc < 4; ++cc) {
-                const char* a0 = vl + (cc * 16) * kVRow + db * 64;
-                i32x2 lo = read_tr(a0);
-                i32x2 up = read_tr(a0 + 8 * kVRow);
-                i32x4 av = {lo.x, lo.y, up.x, up.y};
-                oacc[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, av), pf[cc], oacc[db],
-                                                                  0, 0, 0);
-            }
+    // Keep the softmax work in its block, next to the PV MFMAs it overlaps,
+    // instead of letting it sink past the rescale branch.
+    auto pin_softmax = [&]() {
+        asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(pf[2]), "v"(pf[3]), "v"(l_run));
     };
 
-    // Pipeline: before iteration j, P_j is in registers, K_{j+1} and V_j are
-    // in LDS. Iteration j computes S_{j+1} and O += V_j P_j, then the softmax
-    // of S_{j+1}, while K_{j+2} and V_{j+1} travel HBM -> VGPR -> LDS.
-    const bool ragged = ntiles * kBN > sk;
+    // One pipeline iteration: S = K_tile(kl) Q^T (16 MFMAs); O += V(vl) P
+    // (16 MFMAs) with the online softmax of S interleaved; P <- softmax(S).
+    // with_pv (std::true_type / std::false_type) selects whether the PV half
+    // runs; it does not for the first tile.
+    auto iterate = [&](auto with_pv, const char* kl, const char* vl, int tile, bool ragged) {
+        constexpr bool kPV = decltype(with_pv)::value;
+        bf16x8 kf[4], vf[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) kf[t] = kread(kl, t);
+        f32x16 s0 = f32x16{}, s1 = f32x16{};
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            if (t & 1)
+                s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[t & 3], qf[t >> 1], s1, 0, 0, 0);
+            else
+                s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[t & 3], qf[t >> 1], s0, 0, 0, 0);
+            if (t + 4 < 16) kf[t & 3] = kread(kl, t + 4);
+            if (kPV && t >= 12) vf[t - 12] = vread(vl, t - 12);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        if (ragged) mask_tail(s0, s1, tile);
+        float mx = 0.f, alpha = 1.f, mc = 0.f, lsum = 0.f;
+        float pe[32];
+        uint32_t pn[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            if constexpr (kPV) {
+                oacc[t >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[t & 3], pf[t & 3], oacc[t >> 2], 0, 0, 0);
+                if (t + 4 < 16) vf[t & 3] = vread(vl, t + 4);
+            }
+            if (t == 0) {
+                mx = s0[0];
+#pragma unroll
+                for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s0[r]);
+            } else if (t == 1) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
+                const f32x2 pr = halves(mx);
+                const float m_new = fmaxf(m_run, fmaxf(pr.x, pr.y));
+                const float m_use = (m_new - m_run) * c > kRescaleThreshold ? m_new : m_run;
+                alpha = fast_exp2((m_run - m_use) * c);
+                m_run = m_use;
+                mc = m_use * c;
+            } else {
+                const int e0 = ((t - 2) * 32) / 14, e1 = ((t - 1) * 32) / 14;
+#pragma unroll
+                for (int e = e0; e < e1; ++e) {
+                    const float sv = e < 16 ? s0[e & 15] : s1[e & 15];
+                    pe[e] = fast_exp2(__builtin_fmaf(sv, c, -mc));
+                    lsum += pe[e];
+                    if (e & 1) pn[e >> 1] = pack_bf16x2(pe[e - 1], pe[e]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+            pf[cc] = __builtin_bit_cast(bf16x8, i32x4{(int)pn[4 * cc], (int)pn[4 * cc + 1], (int)pn[4 * cc + 2],
+                                                      (int)pn[4 * cc + 3]});
+        l_run = __builtin_fmaf(l_run, alpha, lsum);
+        pin_softmax();
+        rescale(alpha);
+    };
+
+    // O += V(vl) P for the last tile.
+    auto pv_last = [&](const char* vl) {
+#pragma unroll
+        for (int t = 0; t < 16; ++t)
+            oacc[t >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vread(vl, t), pf[t & 3], oacc[t >> 2], 0, 0, 0);
+    };
+
+    // Pipeline: iteration j reads K_{j+1} and V_j and issues the DMA of
+    // K_{j+3} and V_{j+2} (two K + two V loads per wave; tiles past the end
+    // are read as zeros and never used). At its end, vmcnt(4) leaves only
+    // its own loads in flight: everything iteration j+1 reads has landed.
     if (ntiles > 0) {
-        load_k(0);
-        load_v(0);
-        store_k(0);
-        store_v(0);
-        if (ntiles > 1) {
-            load_k(1);
-            store_k(1);
-        }
-        __syncthreads();
-        f32x16 s[2];
-        qk(0, s);
-        softmax(s, 0, ntiles == 1 && ragged);
-        __syncthreads();  // K stage 0 is refilled in the first iteration
+        dma_k(0);
+        dma_v(0);
+        dma_k(1);
+        dma_v(1);
+        dma_k(2);
+        wait_vmcnt<0>();
+        barrier();
+        iterate(std::false_type{}, kst, vst, 0, ntiles == 1 && ntiles * kBN > sk);
+        barrier();  // K stage 0 is refilled by the first iteration
     }
+    const bool ragged = ntiles * kBN > sk;
     int j = 0;
-    for (; j + 2 < ntiles; ++j) {  // steady state: tiles j+1 and j+2 exist
-        load_k(j + 2);
-        load_v(j + 1);
-        f32x16 s[2];
-        qk((j + 1) & 1, s);
-        pv(j & 1);
-        const float alpha = softmax(s, j + 1, false);
-        // Issue order for the block above: the HBM loads, then each QK^T MFMA
-        // behind its K fragment read, then each PV MFMA behind its two
-        // transpose reads followed by a slice of the softmax VALU work, so the
-        // softmax issues while the PV MFMAs execute.
-        __builtin_amdgcn_sched_group_barrier(0x020, 8, 0);  // VMEM read
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // VALU
-        }
-        pin_softmax();
-        rescale(alpha);
-        store_k(j & 1);
-        store_v((j + 1) & 1);
-        __syncthreads();
+    for (; j + 2 < ntiles; ++j) {
+        dma_k(j + 3);
+        dma_v(j + 2);
+        iterate(std::true_type{}, kst + ((j + 1) % kStages) * kTile, vst + (j % kStages) * kTile, j + 1, false);
+        wait_vmcnt<2 * kDmaPerTile>();
+        barrier();
     }
-    if (j + 1 < ntiles) {  // j = ntiles - 2: the last tile is loaded, no K beyond
-        load_v(j + 1);
-        f32x16 s[2];
-        qk((j + 1) & 1, s);
-        pv(j & 1);
-        const float alpha = softmax(s, j + 1, ragged);
-        pin_softmax();
-        rescale(alpha);
-        store_v((j + 1) & 1);
-        __syncthreads();
+    if (j + 1 < ntiles) {  // j = ntiles - 2: the last tile may be ragged
+        dma_k(j + 3);
+        dma_v(j + 2);
+        iterate(std::true_type{}, kst + ((j + 1) % kStages) * kTile, vst + (j % kStages) * kTile, j + 1, ragged);
+        wait_vmcnt<2 * kDmaPerTile>();
+        barrier();
         ++j;
     }
-    if (j < ntiles) pv(j & 1);  // j = ntiles - 1
+    if (j < ntiles) pv_last(vst + (j % kStages) * kTile);  // j = ntiles - 1
+    wait_vmcnt<0>();  // no LDS DMA may still land after the workgroup ends
 
     // Epilogue: combine the two halves' partial sums, normalise, store.
     {
@@ -330,6 +346,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
 }  // namespace
 
 int attn_fwd_block_m() { return kBM; }
+int attn_fwd_row_margin() { return kBM + kBN * (kStages + 1); }
 
 hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
     const int64_t blocks = (int64_t)p.n_qtiles * p.heads * p.n_groups;

@@ -94,10 +94,11 @@ int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
         p.seqlen_k = (int32_t)a->seqlen_k;
     }
     // Every (batch, head) view is addressed with 32-bit byte offsets that may
-    // run up to one tile past the last row.
+    // run a few tiles past the last row.
     const int64_t rows[4] = {rows_q, rows_k, rows_k, rows_q};
+    const int64_t margin = h3a::attn_fwd_row_margin();
     for (int i = 0; i < 4; ++i) {
-        const int64_t span = (rows[i] + bm + 64) * st[i][1] * 2;
+        const int64_t span = (rows[i] + margin) * st[i][1] * 2;
         if (span >= kMaxSpan)
             return fail(H3A_EUNSUPPORTED, "h3a_attn_fwd: %s view spans %lld bytes (limit 2^31)", nm[i], (long long)span);
     }

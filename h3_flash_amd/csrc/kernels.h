@@ -30,6 +30,9 @@ struct AttnParams {
 };
 
 int attn_fwd_block_m();
+// Rows past the end of a sequence that the kernel may address (all reads there
+// are bounds-checked buffer loads returning zero).
+int attn_fwd_row_margin();
 hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream);
 
 struct QkNormRopeParams {
