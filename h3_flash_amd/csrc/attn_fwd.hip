@@ -11,8 +11,8 @@
 //     query column per lane, so the row max / row sum of the online softmax
 //     are in-lane reductions plus one v_permlane32_swap across wave halves;
 //   * K and V tiles of 64 keys go HBM -> LDS directly (buffer_load ... lds,
-//     16 bytes per lane, no VGPR staging) into three LDS stages each, issued
-//     two tiles ahead of use, so a full iteration hides the load latency;
+//     16 bytes per lane, no VGPR staging) into four LDS stages each, issued
+//     three tiles ahead of use, so two iterations hide the load latency;
 //     one barrier per tile, after each wave's own loads of the previous
 //     iteration are complete (s_waitcnt vmcnt);
 //   * the PV product O^T = V^T P^T takes its A operand with the gfx950
@@ -42,7 +42,7 @@ constexpr int kBM = 256;           // query rows per workgroup
 constexpr int kBN = 64;            // keys per tile
 constexpr int kWaves = 8;
 constexpr int kThreads = kWaves * 64;
-constexpr int kStages = 3;
+constexpr int kStages = 4;
 constexpr int kRow = kD * 2;       // LDS bytes per K / V row
 constexpr int kTile = kBN * kRow;  // 16384
 constexpr int kLdsBytes = 2 * kStages * kTile;
@@ -50,6 +50,7 @@ constexpr int kDmaPerTile = kBN / (kWaves * 4);  // 4-row DMA loads per wave per
 constexpr float kRescaleThreshold = 8.0f;        // log2 units
 
 static_assert(kDmaPerTile == 2, "vmcnt accounting below assumes 2 K + 2 V loads per iteration");
+static_assert(kStages == 4, "the pipeline below is unrolled over four stages");
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
@@ -81,12 +82,12 @@ __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory
 
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
-    char* const kst = smem;                    // K stages 0..2
-    char* const vst = smem + kStages * kTile;  // V stages 0..2
+    char* const kst = smem;                    // K stages 0..3
+    char* const vst = smem + kStages * kTile;  // V stages 0..3
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hi = lane >> 5;  // wave half
     const int l32 = lane & 31;
 
@@ -133,23 +134,26 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
 
     // DMA map: wave w fills rows 8w .. 8w+7 of a tile with two 4-row loads;
     // lane L writes LDS chunk (L & 15) of row r0 + (L >> 4), which holds the
-    // tile's chunk (L & 15) ^ swz(row) of that key row.
-    int dma_off[kDmaPerTile];
+    // tile's chunk (L & 15) ^ swz(row) of that key row. The per-lane byte
+    // offset inside a tile is fixed; the tile's first row adds a uniform term.
+    // Rows past the end of the view are out of the buffer's range: zeros.
+    uint32_t dk[kDmaPerTile], dv[kDmaPerTile];
 #pragma unroll
     for (int i = 0; i < kDmaPerTile; ++i) {
         const int r = (wave * kDmaPerTile + i) * 4 + (lane >> 4);
-        dma_off[i] = ((lane & 15) ^ swz(r)) << 4;
+        const int chunk = ((lane & 15) ^ swz(r)) << 4;
+        dk[i] = (uint32_t)(r * p.k_rs + chunk);
+        dv[i] = (uint32_t)(r * p.v_rs + chunk);
     }
-    auto dma = [&](__amdgpu_buffer_rsrc_t rsrc, int row_bytes, char* stage, int tile) {
+    auto dma = [&](__amdgpu_buffer_rsrc_t rsrc, int row_bytes, const uint32_t* lanes, char* stage, int tile) {
+        const uint32_t skip = (uint32_t)(tile * kBN * row_bytes);
 #pragma unroll
-        for (int i = 0; i < kDmaPerTile; ++i) {
-            const int r0 = (wave * kDmaPerTile + i) * 4;
-            const uint32_t voff = (uint32_t)((tile * kBN + r0 + (lane >> 4)) * row_bytes + dma_off[i]);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(stage + r0 * kRow), 16, voff, 0, 0, 0);
-        }
+        for (int i = 0; i < kDmaPerTile; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(stage + (wave * kDmaPerTile + i) * 4 * kRow),
+                                                     16, lanes[i] + skip, 0, 0, 0);
     };
-    auto dma_k = [&](int tile) { dma(rk, p.k_rs, kst + (tile % kStages) * kTile, tile); };
-    auto dma_v = [&](int tile) { dma(rv, p.v_rs, vst + (tile % kStages) * kTile, tile); };
+    auto dma_k = [&](int tile, int stage) { dma(rk, p.k_rs, dk, kst + stage * kTile, tile); };
+    auto dma_v = [&](int tile, int stage) { dma(rv, p.v_rs, dv, vst + stage * kTile, tile); };
 
     // K fragment of QK^T MFMA t (key block t & 1, head-dim step t >> 1): row
     // 32*(t & 1) + l32, logical chunk 2*(t >> 1) + hi.
@@ -177,7 +181,6 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     for (int db = 0; db < 4; ++db) oacc[db] = f32x16{};
     float m_run = -INFINITY;  // running max of raw scores for this lane's query
     float l_run = 0.f;        // this lane's partial sum (its half of the keys)
-    bf16x8 pf[4];             // P^T of the tile waiting for its PV product
 
     auto kread = [&](const char* kl, int t) {
         return *(const bf16x8*)(kl + (t & 1) * 32 * kRow + (kbase ^ (32 * (t >> 1))));
@@ -206,17 +209,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
                 for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
         }
     };
-    // Keep the softmax work in its block, next to the PV MFMAs it overlaps,
-    // instead of letting it sink past the rescale branch.
-    auto pin_softmax = [&]() {
-        asm volatile("" ::"v"(pf[0]), "v"(pf[1]), "v"(pf[2]), "v"(pf[3]), "v"(l_run));
-    };
 
-    // One pipeline iteration: S = K_tile(kl) Q^T (16 MFMAs); O += V(vl) P
-    // (16 MFMAs) with the online softmax of S interleaved; P <- softmax(S).
+    // One pipeline iteration: S = K_tile(kl) Q^T (16 MFMAs); O += V(vl) P_in
+    // (16 MFMAs) with the online softmax of S interleaved; P_out <- softmax(S).
     // with_pv (std::true_type / std::false_type) selects whether the PV half
-    // runs; it does not for the first tile.
-    auto iterate = [&](auto with_pv, const char* kl, const char* vl, int tile, bool ragged) {
+    // runs; it does not for the first tile. Keys past the end of the
+    // sequence (ragged last tile, padding tiles) are masked to -inf.
+    auto iterate = [&](auto with_pv, const char* kl, const char* vl, int tile, const bf16x8* pin,
+                       bf16x8* pout) __attribute__((always_inline)) {
         constexpr bool kPV = decltype(with_pv)::value;
         bf16x8 kf[4], vf[4];
 #pragma unroll
@@ -232,14 +232,18 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
             if (kPV && t >= 12) vf[t - 12] = vread(vl, t - 12);
             __builtin_amdgcn_sched_barrier(0);
         }
-        if (ragged) mask_tail(s0, s1, tile);
+        if ((tile + 1) * kBN > sk) {
+            // A real branch, not per-element selects: only the last tiles take it.
+            asm volatile("" ::: "memory");
+            mask_tail(s0, s1, tile);
+        }
         float mx = 0.f, alpha = 1.f, mc = 0.f, lsum = 0.f;
         float pe[32];
         uint32_t pn[16];
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
             if constexpr (kPV) {
-                oacc[t >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[t & 3], pf[t & 3], oacc[t >> 2], 0, 0, 0);
+                oacc[t >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[t & 3], pin[t & 3], oacc[t >> 2], 0, 0, 0);
                 if (t + 4 < 16) vf[t & 3] = vread(vl, t + 4);
             }
             if (t == 0) {
@@ -252,7 +256,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
                 const f32x2 pr = halves(mx);
                 const float m_new = fmaxf(m_run, fmaxf(pr.x, pr.y));
                 const float m_use = (m_new - m_run) * c > kRescaleThreshold ? m_new : m_run;
-                alpha = fast_exp2((m_run - m_use) * c);
+                alpha = m_use == m_run ? 1.0f : fast_exp2((m_run - m_use) * c);
                 m_run = m_use;
                 mc = m_use * c;
             } else {
@@ -269,53 +273,55 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         }
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc)
-            pf[cc] = __builtin_bit_cast(bf16x8, i32x4{(int)pn[4 * cc], (int)pn[4 * cc + 1], (int)pn[4 * cc + 2],
-                                                      (int)pn[4 * cc + 3]});
+            pout[cc] = __builtin_bit_cast(bf16x8, i32x4{(int)pn[4 * cc], (int)pn[4 * cc + 1], (int)pn[4 * cc + 2],
+                                                        (int)pn[4 * cc + 3]});
         l_run = __builtin_fmaf(l_run, alpha, lsum);
-        pin_softmax();
+        // Keep the softmax work in its block, next to the PV MFMAs it
+        // overlaps, instead of letting it sink past the rescale branch.
+        asm volatile("" ::"v"(pout[0]), "v"(pout[1]), "v"(pout[2]), "v"(pout[3]), "v"(l_run));
         rescale(alpha);
     };
 
-    // O += V(vl) P for the last tile.
-    auto pv_last = [&](const char* vl) {
-#pragma unroll
-        for (int t = 0; t < 16; ++t)
-            oacc[t >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vread(vl, t), pf[t & 3], oacc[t >> 2], 0, 0, 0);
-    };
-
-    // Pipeline: iteration j reads K_{j+1} and V_j and issues the DMA of
-    // K_{j+3} and V_{j+2} (two K + two V loads per wave; tiles past the end
-    // are read as zeros and never used). At its end, vmcnt(4) leaves only
-    // its own loads in flight: everything iteration j+1 reads has landed.
+    // Pipeline: K_t and V_t live in LDS stage t % 4. Iteration j reads K_{j+1}
+    // and V_j and issues the DMA of K_{j+4} and V_{j+3} (two K + two V loads
+    // per wave); at its end vmcnt(8) leaves only the loads of iterations j-1
+    // and j in flight, so everything iteration j+1 reads has landed. The loop
+    // runs a multiple of 4 iterations, unrolled so that every stage offset is
+    // a compile-time constant and P ping-pongs between two register sets;
+    // tiles past the end read as zeros and are fully masked.
+    bf16x8 pfa[4], pfb[4];
+    const int nsteps = (ntiles + 3) & ~3;
     if (ntiles > 0) {
-        dma_k(0);
-        dma_v(0);
-        dma_k(1);
-        dma_v(1);
-        dma_k(2);
-        wait_vmcnt<0>();
+        dma_k(0, 0);
+        dma_v(0, 0);
+        dma_k(1, 1);
+        dma_v(1, 1);
+        dma_k(2, 2);
+        dma_v(2, 2);
+        dma_k(3, 3);
+        wait_vmcnt<6 * kDmaPerTile>();  // Q and K_0 have landed
         barrier();
-        iterate(std::false_type{}, kst, vst, 0, ntiles == 1 && ntiles * kBN > sk);
-        barrier();  // K stage 0 is refilled by the first iteration
+        iterate(std::false_type{}, kst, vst, 0, pfb, pfa);
+        wait_vmcnt<4 * kDmaPerTile>();  // V_0 and K_1 too
+        barrier();                      // and K stage 0 may be refilled
     }
-    const bool ragged = ntiles * kBN > sk;
-    int j = 0;
-    for (; j + 2 < ntiles; ++j) {
-        dma_k(j + 3);
-        dma_v(j + 2);
-        iterate(std::true_type{}, kst + ((j + 1) % kStages) * kTile, vst + (j % kStages) * kTile, j + 1, false);
-        wait_vmcnt<2 * kDmaPerTile>();
+    auto step = [&](auto u, int jj) __attribute__((always_inline)) {
+        constexpr int U = decltype(u)::value;
+        dma_k(jj + 4, U);
+        dma_v(jj + 3, (U + 3) & 3);
+        if constexpr (U & 1)
+            iterate(std::true_type{}, kst + ((U + 1) & 3) * kTile, vst + U * kTile, jj + 1, pfb, pfa);
+        else
+            iterate(std::true_type{}, kst + ((U + 1) & 3) * kTile, vst + U * kTile, jj + 1, pfa, pfb);
+        wait_vmcnt<4 * kDmaPerTile>();
         barrier();
+    };
+    for (int j = 0; j < nsteps; j += 4) {
+        step(std::integral_constant<int, 0>{}, j);
+        step(std::integral_constant<int, 1>{}, j + 1);
+        step(std::integral_constant<int, 2>{}, j + 2);
+        step(std::integral_constant<int, 3>{}, j + 3);
     }
-    if (j + 1 < ntiles) {  // j = ntiles - 2: the last tile may be ragged
-        dma_k(j + 3);
-        dma_v(j + 2);
-        iterate(std::true_type{}, kst + ((j + 1) % kStages) * kTile, vst + (j % kStages) * kTile, j + 1, ragged);
-        wait_vmcnt<2 * kDmaPerTile>();
-        barrier();
-        ++j;
-    }
-    if (j < ntiles) pv_last(vst + (j % kStages) * kTile);  // j = ntiles - 1
     wait_vmcnt<0>();  // no LDS DMA may still land after the workgroup ends
 
     // Epilogue: combine the two halves' partial sums, normalise, store.
@@ -346,7 +352,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
 }  // namespace
 
 int attn_fwd_block_m() { return kBM; }
-int attn_fwd_row_margin() { return kBM + kBN * (kStages + 1); }
+int attn_fwd_row_margin() { return kBM + kBN * (2 * kStages + 2); }
 
 hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
     const int64_t blocks = (int64_t)p.n_qtiles * p.heads * p.n_groups;
