@@ -55,6 +55,8 @@ static_assert(kStages == 4, "the pipeline below is unrolled over four stages");
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) char lds_char;
+typedef __attribute__((address_space(3))) bf16x8 lds_bf16x8;
 
 __device__ __forceinline__ uint32_t span_bytes(int rows, int row_bytes) {
     return rows > 0 ? (uint32_t)((rows - 1) * row_bytes + kD * 2) : 0u;
@@ -64,7 +66,7 @@ __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 
 
 // Four bf16 of one head-dim column: within each 16-lane group lane i receives
 // element (i & 3) of the 8-byte chunks addressed by lanes 4j + (i >> 2).
-__device__ __forceinline__ i32x2 read_tr(const char* p) {
+__device__ __forceinline__ i32x2 read_tr(const lds_char* p) {
     s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
     return __builtin_bit_cast(i32x2, v);
 }
@@ -82,8 +84,11 @@ __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory
 
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
-    char* const kst = smem;                    // K stages 0..3
-    char* const vst = smem + kStages * kTile;  // V stages 0..3
+    // V stages 0..3 first, then K stages 0..3: with a per-lane base in a VGPR
+    // every fragment read offset then fits the 16-bit ds_read immediate.
+    char* const vst = smem;
+    char* const kst = smem + kStages * kTile;
+    const lds_char* const lds = (const lds_char*)smem;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -182,14 +187,28 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     float m_run = -INFINITY;  // running max of raw scores for this lane's query
     float l_run = 0.f;        // this lane's partial sum (its half of the keys)
 
-    auto kread = [&](const char* kl, int t) {
-        return *(const bf16x8*)(kl + (t & 1) * 32 * kRow + (kbase ^ (32 * (t >> 1))));
+    // Per-lane LDS byte offsets of the K fragments (one per head-dim step)
+    // and of the V transpose reads (one per head-dim block and key half); the
+    // empty asm keeps each in a register so stage and step offsets become
+    // instruction immediates.
+    uint32_t kofs[8], vofs[8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) {
+        kofs[ks] = (uint32_t)(kStages * kTile + (kbase ^ (32 * ks)));
+        asm volatile("" : "+v"(kofs[ks]));
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        vofs[i] = (uint32_t)(vbase ^ (64 * (i >> 1)) ^ (32 * (i & 1)));
+        asm volatile("" : "+v"(vofs[i]));
+    }
+    auto kread = [&](int stage, int t) {
+        return *(const lds_bf16x8*)(lds + kofs[t >> 1] + (stage * kTile + (t & 1) * 32 * kRow));
     };
-    auto vread = [&](const char* vl, int t) {
-        const char* a = vl + (t & 3) * 16 * kRow;
-        const int x = vbase ^ (64 * (t >> 2));
-        const i32x2 lo = read_tr(a + x);
-        const i32x2 up = read_tr(a + 8 * kRow + (x ^ 32));
+    auto vread = [&](int stage, int t) {
+        const lds_char* a = lds + (stage * kTile + (t & 3) * 16 * kRow);
+        const i32x2 lo = read_tr(a + vofs[2 * (t >> 2)]);
+        const i32x2 up = read_tr(a + 8 * kRow + vofs[2 * (t >> 2) + 1]);
         return __builtin_bit_cast(bf16x8, i32x4{lo.x, lo.y, up.x, up.y});
     };
     auto mask_tail = [&](f32x16& s0, f32x16& s1, int tile) {
@@ -210,12 +229,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         }
     };
 
-    // One pipeline iteration: S = K_tile(kl) Q^T (16 MFMAs); O += V(vl) P_in
+    // One pipeline iteration: S = K_tile(K stage kl) Q^T (16 MFMAs); O += V(V stage vl) P_in
     // (16 MFMAs) with the online softmax of S interleaved; P_out <- softmax(S).
     // with_pv (std::true_type / std::false_type) selects whether the PV half
     // runs; it does not for the first tile. Keys past the end of the
     // sequence (ragged last tile, padding tiles) are masked to -inf.
-    auto iterate = [&](auto with_pv, const char* kl, const char* vl, int tile, const bf16x8* pin,
+    auto iterate = [&](auto with_pv, int kl, int vl, int tile, const bf16x8* pin,
                        bf16x8* pout) __attribute__((always_inline)) {
         constexpr bool kPV = decltype(with_pv)::value;
         bf16x8 kf[4], vf[4];
@@ -301,7 +320,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         dma_k(3, 3);
         wait_vmcnt<6 * kDmaPerTile>();  // Q and K_0 have landed
         barrier();
-        iterate(std::false_type{}, kst, vst, 0, pfb, pfa);
+        iterate(std::false_type{}, 0, 0, 0, pfb, pfa);
         wait_vmcnt<4 * kDmaPerTile>();  // V_0 and K_1 too
         barrier();                      // and K stage 0 may be refilled
     }
@@ -310,9 +329,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         dma_k(jj + 4, U);
         dma_v(jj + 3, (U + 3) & 3);
         if constexpr (U & 1)
-            iterate(std::true_type{}, kst + ((U + 1) & 3) * kTile, vst + U * kTile, jj + 1, pfb, pfa);
+            iterate(std::true_type{}, (U + 1) & 3, U, jj + 1, pfb, pfa);
         else
-            iterate(std::true_type{}, kst + ((U + 1) & 3) * kTile, vst + U * kTile, jj + 1, pfa, pfb);
+            iterate(std::true_type{}, (U + 1) & 3, U, jj + 1, pfa, pfb);
         wait_vmcnt<4 * kDmaPerTile>();
         barrier();
     };
