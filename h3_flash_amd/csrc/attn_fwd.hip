@@ -229,109 +229,145 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         }
     };
 
-    // One pipeline iteration: S = K_tile(K stage kl) Q^T (16 MFMAs); O += V(V stage vl) P_in
-    // (16 MFMAs) with the online softmax of S interleaved; P_out <- softmax(S).
-    // with_pv (std::true_type / std::false_type) selects whether the PV half
-    // runs; it does not for the first tile. Keys past the end of the
-    // sequence (ragged last tile, padding tiles) are masked to -inf.
-    auto iterate = [&](auto with_pv, int kl, int vl, int tile, const bf16x8* pin,
-                       bf16x8* pout) __attribute__((always_inline)) {
-        constexpr bool kPV = decltype(with_pv)::value;
-        bf16x8 kf[4], vf[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) kf[t] = kread(kl, t);
-        f32x16 s0 = f32x16{}, s1 = f32x16{};
-#pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            if (t & 1)
-                s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[t & 3], qf[t >> 1], s1, 0, 0, 0);
-            else
-                s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[t & 3], qf[t >> 1], s0, 0, 0, 0);
-            if (t + 4 < 16) kf[t & 3] = kread(kl, t + 4);
-            if (kPV && t >= 12) vf[t - 12] = vread(vl, t - 12);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        if ((tile + 1) * kBN > sk) {
-            // A real branch, not per-element selects: only the last tiles take it.
-            asm volatile("" ::: "memory");
-            mask_tail(s0, s1, tile);
+    // One pipeline iteration, three stages wide: the 16 QK^T MFMAs of a tile
+    // (K stage kl) into s_out, the 16 PV MFMAs of an older tile (V stage vl,
+    // P fragments pin), and the online softmax of the tile in between (s_in,
+    // tile sm_tile) cut into one slice per MFMA, so its VALU work issues under
+    // all 32 MFMAs: slices 0-1 reduce the row max, the others exponentiate
+    // one or two scores each and pack them to bf16 into pout. Each part is
+    // switched on by a std::true_type / std::false_type argument (the
+    // pipeline prologue runs subsets). Keys past the end of the sequence
+    // (ragged last tile, padding tiles) are masked to -inf.
+    auto iterate = [&](auto qk_on, auto sm_on, auto pv_on, int kl, int vl, int sm_tile, f32x16* s_in, f32x16* s_out,
+                       const bf16x8* pin, bf16x8* pout) __attribute__((always_inline)) {
+        constexpr bool kQK = decltype(qk_on)::value;
+        constexpr bool kSM = decltype(sm_on)::value;
+        constexpr bool kPV = decltype(pv_on)::value;
+        constexpr int kSlices = (kQK ? 16 : 0) + (kPV ? 16 : 0);
+        static_assert(!kSM || kSlices >= 16, "the softmax needs at least 16 slices");
+        if constexpr (kSM) {
+            if ((sm_tile + 1) * kBN > sk) {
+                // A real branch, not per-element selects: only the last tiles take it.
+                asm volatile("" ::: "memory");
+                mask_tail(s_in[0], s_in[1], sm_tile);
+            }
         }
         float mx = 0.f, alpha = 1.f, mc = 0.f, lsum = 0.f;
         float pe[32];
         uint32_t pn[16];
+        auto slice = [&](int k) __attribute__((always_inline)) {
+            if constexpr (kSM) {
+                if (k == 0) {
+                    mx = s_in[0][0];
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            if constexpr (kPV) {
-                oacc[t >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[t & 3], pin[t & 3], oacc[t >> 2], 0, 0, 0);
-                if (t + 4 < 16) vf[t & 3] = vread(vl, t + 4);
-            }
-            if (t == 0) {
-                mx = s0[0];
+                    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s_in[0][r]);
+                } else if (k == 1) {
 #pragma unroll
-                for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s0[r]);
-            } else if (t == 1) {
+                    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_in[1][r]);
+                    const f32x2 pr = halves(mx);
+                    const float m_new = fmaxf(m_run, fmaxf(pr.x, pr.y));
+                    const float m_use = (m_new - m_run) * c > kRescaleThreshold ? m_new : m_run;
+                    alpha = m_use == m_run ? 1.0f : fast_exp2((m_run - m_use) * c);
+                    m_run = m_use;
+                    mc = m_use * c;
+                } else {
+                    const int e0 = ((k - 2) * 32) / (kSlices - 2), e1 = ((k - 1) * 32) / (kSlices - 2);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s1[r]);
-                const f32x2 pr = halves(mx);
-                const float m_new = fmaxf(m_run, fmaxf(pr.x, pr.y));
-                const float m_use = (m_new - m_run) * c > kRescaleThreshold ? m_new : m_run;
-                alpha = m_use == m_run ? 1.0f : fast_exp2((m_run - m_use) * c);
-                m_run = m_use;
-                mc = m_use * c;
-            } else {
-                const int e0 = ((t - 2) * 32) / 14, e1 = ((t - 1) * 32) / 14;
-#pragma unroll
-                for (int e = e0; e < e1; ++e) {
-                    const float sv = e < 16 ? s0[e & 15] : s1[e & 15];
-                    pe[e] = fast_exp2(__builtin_fmaf(sv, c, -mc));
-                    lsum += pe[e];
-                    if (e & 1) pn[e >> 1] = pack_bf16x2(pe[e - 1], pe[e]);
+                    for (int e = e0; e < e1; ++e) {
+                        const float sv = s_in[e >> 4][e & 15];
+                        pe[e] = fast_exp2(__builtin_fmaf(sv, c, -mc));
+                        lsum = e == 0 ? pe[e] : lsum + pe[e];
+                        if (e & 1) pn[e >> 1] = pack_bf16x2(pe[e - 1], pe[e]);
+                    }
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);
-        }
+        };
+        bf16x8 kf[4], vf[4];
+        if constexpr (kQK) {
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc)
-            pout[cc] = __builtin_bit_cast(bf16x8, i32x4{(int)pn[4 * cc], (int)pn[4 * cc + 1], (int)pn[4 * cc + 2],
-                                                        (int)pn[4 * cc + 3]});
-        l_run = __builtin_fmaf(l_run, alpha, lsum);
-        // Keep the softmax work in its block, next to the PV MFMAs it
-        // overlaps, instead of letting it sink past the rescale branch.
-        asm volatile("" ::"v"(pout[0]), "v"(pout[1]), "v"(pout[2]), "v"(pout[3]), "v"(l_run));
-        rescale(alpha);
+            for (int t = 0; t < 4; ++t) kf[t] = kread(kl, t);
+            s_out[0] = f32x16{};
+            s_out[1] = f32x16{};
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                s_out[t & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[t & 3], qf[t >> 1], s_out[t & 1], 0, 0, 0);
+                if (t + 4 < 16) kf[t & 3] = kread(kl, t + 4);
+                if (kPV && t >= 12) vf[t - 12] = vread(vl, t - 12);
+                slice(t);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        if constexpr (kPV) {
+            if constexpr (!kQK) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) vf[t] = vread(vl, t);
+            }
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                oacc[t >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[t & 3], pin[t & 3], oacc[t >> 2], 0, 0, 0);
+                if (t + 4 < 16) vf[t & 3] = vread(vl, t + 4);
+                slice((kQK ? 16 : 0) + t);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        if constexpr (kSM) {
+            if constexpr (kSlices == 0) {
+#pragma unroll
+                for (int k = 0; k < 16; ++k) slice(k);
+            }
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc)
+                pout[cc] = __builtin_bit_cast(bf16x8, i32x4{(int)pn[4 * cc], (int)pn[4 * cc + 1], (int)pn[4 * cc + 2],
+                                                            (int)pn[4 * cc + 3]});
+            l_run = __builtin_fmaf(l_run, alpha, lsum);
+            // Keep the softmax work in its block, next to the MFMAs it
+            // overlaps, instead of letting it sink past the rescale branch.
+            asm volatile("" ::"v"(pout[0]), "v"(pout[1]), "v"(pout[2]), "v"(pout[3]), "v"(l_run));
+            // O holds the PV products up to this iteration's, all relative to
+            // the old running max: rescale before the next PV adds to it.
+            rescale(alpha);
+        }
     };
 
-    // Pipeline: K_t and V_t live in LDS stage t % 4. Iteration j reads K_{j+1}
-    // and V_j and issues the DMA of K_{j+4} and V_{j+3} (two K + two V loads
-    // per wave); at its end vmcnt(8) leaves only the loads of iterations j-1
-    // and j in flight, so everything iteration j+1 reads has landed. The loop
-    // runs a multiple of 4 iterations, unrolled so that every stage offset is
-    // a compile-time constant and P ping-pongs between two register sets;
-    // tiles past the end read as zeros and are fully masked.
+    // Pipeline: K_t and V_t live in LDS stage t % 4. Iteration j issues the
+    // QK^T of tile j+2, the softmax of tile j+1 and the PV of tile j, and the
+    // DMA of K_{j+5} (into K_{j+1}'s stage) and V_{j+3} (into V_{j-1}'s). At
+    // its end vmcnt(8) leaves only the loads of iterations j-1 and j in
+    // flight, so K_{j+3} and V_{j+1}, issued at iteration j-2, have landed
+    // before iteration j+1. The loop runs a multiple of 4 iterations,
+    // unrolled so that every stage offset is a compile-time constant and S
+    // and P ping-pong between two register sets each; tiles past the end read
+    // as zeros and are fully masked.
+    f32x16 sa[2], sb[2];
     bf16x8 pfa[4], pfb[4];
     const int nsteps = (ntiles + 3) & ~3;
     if (ntiles > 0) {
         dma_k(0, 0);
-        dma_v(0, 0);
         dma_k(1, 1);
-        dma_v(1, 1);
+        dma_v(0, 0);
         dma_k(2, 2);
-        dma_v(2, 2);
+        dma_v(1, 1);
         dma_k(3, 3);
+        dma_v(2, 2);
         wait_vmcnt<6 * kDmaPerTile>();  // Q and K_0 have landed
         barrier();
-        iterate(std::false_type{}, 0, 0, 0, pfb, pfa);
-        wait_vmcnt<4 * kDmaPerTile>();  // V_0 and K_1 too
-        barrier();                      // and K stage 0 may be refilled
+        iterate(std::true_type{}, std::false_type{}, std::false_type{}, 0, 0, 0, sb, sa, pfb, pfb);
+        barrier();  // K stage 0 is free
+        dma_k(4, 0);
+        wait_vmcnt<6 * kDmaPerTile>();  // K_1 has landed
+        barrier();
+        iterate(std::true_type{}, std::true_type{}, std::false_type{}, 1, 0, 0, sa, sb, pfb, pfa);
+        wait_vmcnt<4 * kDmaPerTile>();  // V_0 and K_2 too
+        barrier();                      // and K stage 1 is free
     }
     auto step = [&](auto u, int jj) __attribute__((always_inline)) {
         constexpr int U = decltype(u)::value;
-        dma_k(jj + 4, U);
+        dma_k(jj + 5, (U + 1) & 3);
         dma_v(jj + 3, (U + 3) & 3);
         if constexpr (U & 1)
-            iterate(std::true_type{}, (U + 1) & 3, U, jj + 1, pfb, pfa);
+            iterate(std::true_type{}, std::true_type{}, std::true_type{}, (U + 2) & 3, U, jj + 1, sa, sb, pfb, pfa);
         else
-            iterate(std::true_type{}, (U + 1) & 3, U, jj + 1, pfa, pfb);
+            iterate(std::true_type{}, std::true_type{}, std::true_type{}, (U + 2) & 3, U, jj + 1, sb, sa, pfa, pfb);
         wait_vmcnt<4 * kDmaPerTile>();
         barrier();
     };
