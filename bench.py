@@ -39,8 +39,8 @@ PMC_SUMMARY = ROOT / "profiles" / "attn_fwd_c2_pmc.txt"
 def parse_args(argv=None):
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--steps", type=int, default=30)
+    p.add_argument("--warmup", type=int, default=10, help="untimed launches; the clock settles after about 8")
     p.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"])
     p.add_argument("--cpu-rows", type=int, default=0, help="query rows in the CPU baseline sample (0: all)")
     p.add_argument("--cpu-repeats", type=int, default=2)

@@ -11,17 +11,17 @@
 //     query column per lane, so the row max / row sum of the online softmax
 //     are in-lane reductions plus one v_permlane32_swap across wave halves;
 //   * K and V tiles of 64 keys go HBM -> LDS directly (buffer_load ... lds,
-//     16 bytes per lane, no VGPR staging) into four LDS stages each, issued
-//     three tiles ahead of use, so two iterations hide the load latency;
-//     one barrier per tile, after each wave's own loads of the previous
-//     iteration are complete (s_waitcnt vmcnt);
+//     16 bytes per lane, no VGPR staging) into four LDS stages each; one
+//     barrier per tile, after each wave's own loads of the previous
+//     iteration are complete (s_waitcnt vmcnt), so every load has a whole
+//     iteration to land;
 //   * the PV product O^T = V^T P^T takes its A operand with the gfx950
 //     transpose read ds_read_b64_tr_b16 (four keys of one head-dim column per
 //     lane) and its B operand (P^T, bf16) straight from the S^T accumulators;
-//   * software pipeline (hand scheduled, sched_barrier fenced): iteration j
-//     issues the 16 QK^T MFMAs of tile j+1 with their K fragments read four
-//     MFMAs ahead, then the 16 PV MFMAs of tile j, each followed by its
-//     transpose reads four MFMAs ahead and a slice of the softmax of tile j+1;
+//   * three-tile software pipeline (hand scheduled, sched_barrier fenced):
+//     iteration j issues the 16 QK^T MFMAs of tile j+2, then the 16 PV MFMAs
+//     of tile j, with K / V fragments read four MFMAs ahead, and spreads the
+//     softmax of tile j+1 (VALU and exp2) in slices between all 32 MFMAs;
 //   * softmax runs in the exp2 domain with fp32 running max / sum; the running
 //     max is only raised when a tile exceeds it by more than 2^8, so the O
 //     rescale is skipped for almost every tile.
