@@ -22,9 +22,13 @@
 //     iteration j issues the 16 QK^T MFMAs of tile j+2, then the 16 PV MFMAs
 //     of tile j, with K / V fragments read four MFMAs ahead, and spreads the
 //     softmax of tile j+1 (VALU and exp2) in slices between all 32 MFMAs;
-//   * softmax runs in the exp2 domain with fp32 running max / sum; the running
-//     max is only raised when a tile exceeds it by more than 2^8, so the O
-//     rescale is skipped for almost every tile.
+//   * softmax runs in the exp2 domain, p = exp2(s*c - mc), with an fp32 row
+//     sum. The offset mc is the first tile's max; later tiles reduce no max:
+//     the row sum bounds every p, and when it passes 2^16 the offset rises
+//     by the sum's binary exponent and P, O and l are scaled by that power
+//     of two, exactly. A tile that overflows (p = inf: a score more than
+//     ~128 log2 units above the offset) is recomputed from K in global
+//     memory against its exact max.
 // LDS rows are 256 bytes, unpadded; the 16-byte chunk c of row r is stored at
 // chunk c ^ swz(r), swz(r) = 4*(r & 3) + ((r >> 2) & 3). Both read patterns are
 // then bank-conflict free: the K reads (16 consecutive rows, one chunk) and the
@@ -47,7 +51,7 @@ constexpr int kRow = kD * 2;       // LDS bytes per K / V row
 constexpr int kTile = kBN * kRow;  // 16384
 constexpr int kLdsBytes = 2 * kStages * kTile;
 constexpr int kDmaPerTile = kBN / (kWaves * 4);  // 4-row DMA loads per wave per tile
-constexpr float kRescaleThreshold = 8.0f;        // log2 units
+constexpr float kSumLimit = 65536.0f;            // row-sum bound of the fast softmax path
 
 static_assert(kDmaPerTile == 2, "vmcnt accounting below assumes 2 K + 2 V loads per iteration");
 static_assert(kStages == 4, "the pipeline below is unrolled over four stages");
@@ -123,9 +127,14 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     const char* qb = (const char*)p.q + 2 * (b * p.q_sb + h * p.q_sh) + (int64_t)q0 * p.q_rs;
     const char* kb = (const char*)p.k + 2 * (b * p.k_sb + h * p.k_sh) + (int64_t)k0 * p.k_rs;
     const char* vb = (const char*)p.v + 2 * (b * p.v_sb + h * p.v_sh) + (int64_t)k0 * p.v_rs;
-    const auto rq = make_rsrc(qb, span_bytes(sq, p.q_rs));
-    const auto rk = make_rsrc(kb, span_bytes(sk, p.k_rs));
-    const auto rv = make_rsrc(vb, span_bytes(sk, p.v_rs));
+    // The Q loads and the K / V DMA are written as inline asm, so the
+    // compiler tracks none of them: it cannot tell the LDS stages apart and
+    // would otherwise wait for every DMA in flight (vmcnt(0)) before the
+    // first LDS read that follows one. Their completion is ordered explicitly
+    // with wait_vmcnt, barriers and register pins below.
+    const i32x4 rq = make_rsrc_words(qb, span_bytes(sq, p.q_rs));
+    const i32x4 rk = make_rsrc_words(kb, span_bytes(sk, p.k_rs));
+    const i32x4 rv = make_rsrc_words(vb, span_bytes(sk, p.v_rs));
 
     // Q fragment: lane holds query row (m0 + 32*wave + l32), head dims
     // 16*ks + 8*hi .. +8 for ks = 0..7 (B operand of S^T = K Q^T).
@@ -133,7 +142,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     bf16x8 qf[8];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
-        i32x4 raw = buf_load16(rq, (uint32_t)(mq * p.q_rs + ks * 32 + hi * 16));
+        i32x4 raw;
+        asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen"
+                     : "=v"(raw)
+                     : "v"((uint32_t)(mq * p.q_rs + ks * 32 + hi * 16)), "s"(rq)
+                     : "memory");
         qf[ks] = __builtin_bit_cast(bf16x8, raw);
     }
 
@@ -150,15 +163,29 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         dk[i] = (uint32_t)(r * p.k_rs + chunk);
         dv[i] = (uint32_t)(r * p.v_rs + chunk);
     }
-    auto dma = [&](__amdgpu_buffer_rsrc_t rsrc, int row_bytes, const uint32_t* lanes, char* stage, int tile) {
+    // buffer_load ... lds writes 16 bytes per lane to LDS address M0 + 16*lane;
+    // M0 needs one wait state before the load reads it. Nothing else in this
+    // kernel uses M0 (it is a reserved register, so it is not listed as
+    // clobbered).
+    auto dma1 = [&](const i32x4& rsrc, int row_bytes, const uint32_t* lanes, char* stage, int tile, int i) {
         const uint32_t skip = (uint32_t)(tile * kBN * row_bytes);
-#pragma unroll
-        for (int i = 0; i < kDmaPerTile; ++i)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(stage + (wave * kDmaPerTile + i) * 4 * kRow),
-                                                     16, lanes[i] + skip, 0, 0, 0);
+        const uint32_t dst = (uint32_t)(uintptr_t)(const lds_char*)(stage + (wave * kDmaPerTile + i) * 4 * kRow);
+        asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                     :
+                     : "s"(dst), "v"(lanes[i] + skip), "s"(rsrc)
+                     : "memory");
     };
-    auto dma_k = [&](int tile, int stage) { dma(rk, p.k_rs, dk, kst + stage * kTile, tile); };
-    auto dma_v = [&](int tile, int stage) { dma(rv, p.v_rs, dv, vst + stage * kTile, tile); };
+    // Load i (of kDmaPerTile) of this wave's share of a K / V tile.
+    auto dma_k1 = [&](int tile, int stage, int i) { dma1(rk, p.k_rs, dk, kst + stage * kTile, tile, i); };
+    auto dma_v1 = [&](int tile, int stage, int i) { dma1(rv, p.v_rs, dv, vst + stage * kTile, tile, i); };
+    auto dma_k = [&](int tile, int stage) {
+#pragma unroll
+        for (int i = 0; i < kDmaPerTile; ++i) dma_k1(tile, stage, i);
+    };
+    auto dma_v = [&](int tile, int stage) {
+#pragma unroll
+        for (int i = 0; i < kDmaPerTile; ++i) dma_v1(tile, stage, i);
+    };
 
     // K fragment of QK^T MFMA t (key block t & 1, head-dim step t >> 1): row
     // 32*(t & 1) + l32, logical chunk 2*(t >> 1) + hi.
@@ -184,7 +211,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     f32x16 oacc[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db) oacc[db] = f32x16{};
-    float m_run = -INFINITY;  // running max of raw scores for this lane's query
+    // Exponent offset of this lane's query, log2 units: p = exp2(s*c - mc).
+    // Set from the first tile's max, raised in whole steps when a tile's
+    // row sum grows past kSumLimit.
+    float mc = 0.f;
     float l_run = 0.f;        // this lane's partial sum (its half of the keys)
 
     // Per-lane LDS byte offsets of the K fragments (one per head-dim step)
@@ -220,21 +250,56 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
             if (key + 32 >= sk) s1[r] = -INFINITY;
         }
     };
-    auto rescale = [&](float alpha) {
-        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+
+    // Redo the softmax of a tile whose exponentials overflowed: S again from
+    // K in global memory (its LDS stage may already hold a newer tile) and
+    // the resident Q, then the exact max of the tile, a new offset at or
+    // above it, and O and l rescaled to that offset. Leaves every p <= 1.
+    const auto rk_plain = make_rsrc(kb, span_bytes(sk, p.k_rs));
+    auto overflow = [&](int tile, bf16x8* pout, float& lsum) __attribute__((always_inline)) {
+        f32x16 s2[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+        for (int t = 0; t < 16; ++t) {
+            const uint32_t row = (uint32_t)(tile * kBN + 32 * (t & 1) + l32);
+            const i32x4 raw = buf_load16(rk_plain, row * (uint32_t)p.k_rs + (t >> 1) * 32 + hi * 16);
+            s2[t & 1] =
+                __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, raw), qf[t >> 1], s2[t & 1], 0, 0, 0);
         }
+        if ((tile + 1) * kBN > sk) mask_tail(s2[0], s2[1], tile);
+        float mx = s2[0][0];
+#pragma unroll
+        for (int e = 1; e < 32; ++e) mx = fmaxf(mx, s2[e >> 4][e & 15]);
+        const f32x2 pr = halves(mx);
+        const float mc_new = fmaxf(mc, fmaxf(pr.x, pr.y) * c);
+        const float alpha = fast_exp2(mc - mc_new);
+        mc = mc_new;
+        lsum = 0.f;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            i32x4 w;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int e = 8 * cc + 2 * i;
+                const float a0 = fast_exp2(__builtin_fmaf(s2[e >> 4][e & 15], c, -mc));
+                const float a1 = fast_exp2(__builtin_fmaf(s2[e >> 4][(e & 15) + 1], c, -mc));
+                lsum += a0 + a1;
+                w[i] = (int)pack_bf16x2(a0, a1);
+            }
+            pout[cc] = __builtin_bit_cast(bf16x8, w);
+        }
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+        l_run *= alpha;
     };
 
     // One pipeline iteration, three stages wide: the 16 QK^T MFMAs of a tile
     // (K stage kl) into s_out, the 16 PV MFMAs of an older tile (V stage vl,
     // P fragments pin), and the online softmax of the tile in between (s_in,
     // tile sm_tile) cut into one slice per MFMA, so its VALU work issues under
-    // all 32 MFMAs: slices 0-1 reduce the row max, the others exponentiate
-    // one or two scores each and pack them to bf16 into pout. Each part is
+    // all 32 MFMAs: each slice exponentiates one or two scores and packs
+    // them to bf16 into pout. Each part is
     // switched on by a std::true_type / std::false_type argument (the
     // pipeline prologue runs subsets). Keys past the end of the sequence
     // (ragged last tile, padding tiles) are masked to -inf.
@@ -243,12 +308,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // names their stage; -1: none) so the next MFMA group starts at once.
     bf16x8 kf[4];
     auto iterate = [&](auto qk_on, auto sm_on, auto pv_on, int kl, int vl, int sm_tile, f32x16* s_in, f32x16* s_out,
-                       const bf16x8* pin, bf16x8* pout, int kl_next) __attribute__((always_inline)) {
+                       const bf16x8* pin, bf16x8* pout, int kl_next, auto&& hook) __attribute__((always_inline)) {
         constexpr bool kQK = decltype(qk_on)::value;
-        constexpr bool kSM = decltype(sm_on)::value;
+        constexpr int kSM = decltype(sm_on)::value;  // 0: none, 1: running offset, 2: first tile
         constexpr bool kPV = decltype(pv_on)::value;
         constexpr int kSlices = (kQK ? 16 : 0) + (kPV ? 16 : 0);
-        static_assert(!kSM || kSlices >= 16, "the softmax needs at least 16 slices");
+        static_assert(kSM == 0 || kSlices >= 16, "the softmax is spread over at least 16 slices");
         if constexpr (kSM) {
             if ((sm_tile + 1) * kBN > sk) {
                 // A real branch, not per-element selects: only the last tiles take it.
@@ -256,11 +321,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
                 mask_tail(s_in[0], s_in[1], sm_tile);
             }
         }
-        float mx = 0.f, alpha = 1.f, mc = 0.f, lsum = 0.f;
+        float lsum = 0.f, mx = 0.f;
         float pe[32];
         uint32_t pn[16];
+        // Each slice exponentiates one score (two without the PV half)
+        // against the offset mc, adds it to the fp32 row sum and packs pairs
+        // to bf16. Only the first tile reduces its max (slices 0-1) to set mc.
+        constexpr int kFirstExp = kSM == 2 ? 2 : 0;
         auto slice = [&](int k) __attribute__((always_inline)) {
-            if constexpr (kSM) {
+            if constexpr (kSM == 2) {
                 if (k == 0) {
                     mx = s_in[0][0];
 #pragma unroll
@@ -269,18 +338,17 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_in[1][r]);
                     const f32x2 pr = halves(mx);
-                    const float m_new = fmaxf(m_run, fmaxf(pr.x, pr.y));
-                    const float m_use = (m_new - m_run) * c > kRescaleThreshold ? m_new : m_run;
-                    alpha = m_use == m_run ? 1.0f : fast_exp2((m_run - m_use) * c);
-                    m_run = m_use;
-                    mc = m_use * c;
-                } else {
-                    const int e0 = ((k - 2) * 32) / (kSlices - 2), e1 = ((k - 1) * 32) / (kSlices - 2);
+                    mc = fmaxf(pr.x, pr.y) * c;  // finite: tile 0 has a key
+                }
+            }
+            if constexpr (kSM != 0) {
+                if (k >= kFirstExp) {
+                    const int e0 = ((k - kFirstExp) * 32) / (kSlices - kFirstExp);
+                    const int e1 = ((k - kFirstExp + 1) * 32) / (kSlices - kFirstExp);
 #pragma unroll
                     for (int e = e0; e < e1; ++e) {
-                        const float sv = s_in[e >> 4][e & 15];
-                        pe[e] = fast_exp2(__builtin_fmaf(sv, c, -mc));
-                        lsum = e == 0 ? pe[e] : lsum + pe[e];
+                        pe[e] = fast_exp2(__builtin_fmaf(s_in[e >> 4][e & 15], c, -mc));
+                        lsum = e == 0 ? pe[e] : lsum + pe[e];  // fp32: l feeds the LSE
                         if (e & 1) pn[e >> 1] = pack_bf16x2(pe[e - 1], pe[e]);
                     }
                 }
@@ -295,6 +363,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
                 s_out[t & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[t & 3], qf[t >> 1], s_out[t & 1], 0, 0, 0);
                 if (t + 4 < 16) kf[t & 3] = kread(kl, t + 4);
                 if (kPV && t >= 12) vf[t - 12] = vread(vl, t - 12);
+                hook(t);
                 slice(t);
                 __builtin_amdgcn_sched_barrier(0);
             }
@@ -309,26 +378,57 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
                 oacc[t >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[t & 3], pin[t & 3], oacc[t >> 2], 0, 0, 0);
                 if (t + 4 < 16) vf[t & 3] = vread(vl, t + 4);
                 if (t >= 12 && kl_next >= 0) kf[t - 12] = kread(kl_next, t - 12);
+                hook((kQK ? 16 : 0) + t);
                 slice((kQK ? 16 : 0) + t);
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
-        if constexpr (kSM) {
-            if constexpr (kSlices == 0) {
-#pragma unroll
-                for (int k = 0; k < 16; ++k) slice(k);
-            }
+        if constexpr (kSM != 0) {
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc)
                 pout[cc] = __builtin_bit_cast(bf16x8, i32x4{(int)pn[4 * cc], (int)pn[4 * cc + 1], (int)pn[4 * cc + 2],
                                                             (int)pn[4 * cc + 3]});
-            l_run = __builtin_fmaf(l_run, alpha, lsum);
             // Keep the softmax work in its block, next to the MFMAs it
-            // overlaps, instead of letting it sink past the rescale branch.
-            asm volatile("" ::"v"(pout[0]), "v"(pout[1]), "v"(pout[2]), "v"(pout[3]), "v"(l_run));
-            // O holds the PV products up to this iteration's, all relative to
-            // the old running max: rescale before the next PV adds to it.
-            rescale(alpha);
+            // overlaps, instead of letting it sink into the branch below.
+            asm volatile("" ::"v"(pout[0]), "v"(pout[1]), "v"(pout[2]), "v"(pout[3]), "v"(lsum));
+            // Every p of the lane is at most its row sum. A sum past
+            // kSumLimit (scores well above the offset) raises the offset of
+            // the query by the sum's binary exponent, for both lanes of the
+            // query: P, O and l are scaled by that power of two, exactly. O
+            // holds this iteration's PV products, all at the old offset, and
+            // the next PV adds this tile's P.
+            if (__builtin_amdgcn_ballot_w64(lsum > kSumLimit)) {
+                asm volatile("" ::: "memory");  // a real branch
+                if (__builtin_amdgcn_ballot_w64(lsum == INFINITY)) {
+                    asm volatile("" ::: "memory");
+                    overflow(sm_tile, pout, lsum);
+                }
+                int ex = lsum > kSumLimit ? __builtin_amdgcn_frexp_expf(lsum) : 0;
+                {
+                    const f32x2 pr = halves(__int_as_float(ex));
+                    ex = max(__float_as_int(pr.x), __float_as_int(pr.y));
+                }
+                const float alpha = __builtin_ldexpf(1.0f, -ex);
+                mc += (float)ex;
+                lsum *= alpha;
+#pragma unroll
+                for (int cc = 0; cc < 4; ++cc) {
+                    i32x4 w = __builtin_bit_cast(i32x4, pout[cc]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const uint32_t u = (uint32_t)w[i];
+                        w[i] = (int)pack_bf16x2(__uint_as_float(u << 16) * alpha,
+                                                __uint_as_float(u & 0xffff0000u) * alpha);
+                    }
+                    pout[cc] = __builtin_bit_cast(bf16x8, w);
+                }
+#pragma unroll
+                for (int db = 0; db < 4; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+                l_run *= alpha;
+            }
+            l_run += lsum;
         }
     };
 
@@ -344,6 +444,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // as zeros and are fully masked.
     f32x16 sa[2], sb[2];
     bf16x8 pfa[4], pfb[4];
+    auto no_hook = [](int) {};
+    constexpr std::integral_constant<int, 0> kNoSoftmax{};
+    constexpr std::integral_constant<int, 1> kSoftmax{};
+    constexpr std::integral_constant<int, 2> kFirstSoftmax{};
     const int nsteps = (ntiles + 3) & ~3;
     if (ntiles > 0) {
         dma_k(0, 0);
@@ -354,17 +458,19 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         dma_k(3, 3);
         dma_v(2, 2);
         wait_vmcnt<6 * kDmaPerTile>();  // Q and K_0 have landed
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) asm volatile("" : "+v"(qf[ks]));  // no Q use before the wait
         barrier();
 #pragma unroll
         for (int t = 0; t < 4; ++t) kf[t] = kread(0, t);
-        iterate(std::true_type{}, std::false_type{}, std::false_type{}, 0, 0, 0, sb, sa, pfb, pfb, -1);
+        iterate(std::true_type{}, kNoSoftmax, std::false_type{}, 0, 0, 0, sb, sa, pfb, pfb, -1, no_hook);
         barrier();  // K stage 0 is free
         dma_k(4, 0);
         wait_vmcnt<6 * kDmaPerTile>();  // K_1 has landed
         barrier();
 #pragma unroll
         for (int t = 0; t < 4; ++t) kf[t] = kread(1, t);
-        iterate(std::true_type{}, std::true_type{}, std::false_type{}, 1, 0, 0, sa, sb, pfb, pfa, -1);
+        iterate(std::true_type{}, kFirstSoftmax, std::false_type{}, 1, 0, 0, sa, sb, pfb, pfa, -1, no_hook);
         wait_vmcnt<2 * kDmaPerTile>();  // V_0, K_2, V_1 and K_3 too
         barrier();                      // and K stage 1 is free
 #pragma unroll
@@ -372,14 +478,20 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     }
     auto step = [&](auto u, int jj) __attribute__((always_inline)) {
         constexpr int U = decltype(u)::value;
-        dma_k(jj + 5, (U + 1) & 3);
-        dma_v(jj + 3, (U + 3) & 3);
+        // The four loads are spread over the iteration so that their LDS
+        // writes do not arrive as one burst that holds up the fragment reads.
+        auto hook = [&](int k) __attribute__((always_inline)) {
+            if (k == 0) dma_k1(jj + 5, (U + 1) & 3, 0);
+            if (k == 8) dma_k1(jj + 5, (U + 1) & 3, 1);
+            if (k == 16) dma_v1(jj + 3, (U + 3) & 3, 0);
+            if (k == 24) dma_v1(jj + 3, (U + 3) & 3, 1);
+        };
         if constexpr (U & 1)
-            iterate(std::true_type{}, std::true_type{}, std::true_type{}, (U + 2) & 3, U, jj + 1, sa, sb, pfb, pfa,
-                    (U + 3) & 3);
+            iterate(std::true_type{}, kSoftmax, std::true_type{}, (U + 2) & 3, U, jj + 1, sa, sb, pfb, pfa,
+                    (U + 3) & 3, hook);
         else
-            iterate(std::true_type{}, std::true_type{}, std::true_type{}, (U + 2) & 3, U, jj + 1, sb, sa, pfa, pfb,
-                    (U + 3) & 3);
+            iterate(std::true_type{}, kSoftmax, std::true_type{}, (U + 2) & 3, U, jj + 1, sb, sa, pfa, pfb,
+                    (U + 3) & 3, hook);
         wait_vmcnt<2 * kDmaPerTile>();
         barrier();
     };
@@ -410,7 +522,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
                 *(i32x2*)(ob + d * 2) = w;
             }
         if (p.lse != nullptr && hi == 0) {
-            const float lse = l_run > 0.f ? (m_run * c + __log2f(l_run)) * 0.69314718055994531f : -INFINITY;
+            const float lse = l_run > 0.f ? (mc + __log2f(l_run)) * 0.69314718055994531f : -INFINITY;
             p.lse[b * p.lse_sb + h * p.lse_sh + q0 + mq] = lse;
         }
     }

@@ -136,6 +136,40 @@ def test_empty_key_range_gives_zero_and_minus_inf():
     assert torch.all(out == 0) and torch.all(torch.isneginf(lse))
 
 
+def _aligned_scores(beta, alpha=30.0, Sq=300, H=2, seed=22):
+    """q rows ~ alpha*u, k rows ~ beta_j*u (plus noise): logits*log2(e)*scale
+    grow like 0.1275*alpha*beta_j along the keys."""
+    g = torch.Generator().manual_seed(seed)
+    S, D = beta.numel(), 128
+    u = torch.randn(D, generator=g)
+    u = u / u.norm()
+    q = (alpha * u + 0.05 * torch.randn((1, Sq, H, D), generator=g)).to(torch.bfloat16)
+    k = (beta[None, :, None, None] * u + 0.05 * torch.randn((1, S, H, D), generator=g)).to(torch.bfloat16)
+    v = torch.randn((1, S, H, D), generator=g).to(torch.bfloat16)
+    return q, k, v
+
+
+def test_scores_rising_along_the_keys():
+    # ~120 log2 units of growth after the first tile: several whole-exponent
+    # raises of the softmax offset, each rescaling P, O and l
+    q, k, v = _aligned_scores(torch.linspace(0.0, 31.0, 1000))
+    out, lse = run(q, k, v)
+    ref_o, ref_l = sdpa_reference(q, k, v)
+    assert_parity(out, lse, ref_o, ref_l, "rising")
+
+
+def test_score_jump_past_exponent_range():
+    # ~300 log2 units above every earlier key: exp2 overflows and the tile is
+    # recomputed against its exact max; once in a middle tile, once in the last
+    for pos in (400, 990):
+        beta = torch.zeros(1000)
+        beta[pos:pos + 10] = 80.0
+        q, k, v = _aligned_scores(beta, seed=23 + pos)
+        out, lse = run(q, k, v)
+        ref_o, ref_l = sdpa_reference(q, k, v)
+        assert_parity(out, lse, ref_o, ref_l, ("jump", pos))
+
+
 def test_unsupported_requests_raise():
     q = _rand((1, 8, 2, 128), 15).to(DEV)
     with pytest.raises(RuntimeError, match="non-causal"):
