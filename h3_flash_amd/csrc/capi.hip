@@ -161,6 +161,12 @@ int h3a_qknorm_rope(const h3a_qknorm_rope_args* a, void* stream) {
     p.seqlen = (int32_t)a->seqlen; p.heads = (int32_t)a->heads; p.n_tensors = n;
     p.head_dim = (int32_t)D; p.rotary_dim = (int32_t)R; p.w_f32 = a->w_dtype == H3A_DTYPE_F32;
     p.rows = a->batch * a->seqlen * n * a->heads;
+    if (p.rows >= ((int64_t)1 << 31) || a->batch > 65535)
+        return fail(H3A_EUNSUPPORTED, "h3a_qknorm_rope: %lld rows, batch %lld (limits 2^31, 65535)", (long long)p.rows,
+                    (long long)a->batch);
+    p.div_heads = h3a::make_fast_div((uint32_t)a->heads);
+    p.div_tensors = h3a::make_fast_div((uint32_t)n);
+    p.div_seqlen = h3a::make_fast_div((uint32_t)a->seqlen);
     hipError_t e = h3a::launch_qknorm_rope(p, (hipStream_t)stream);
     if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_qknorm_rope: launch failed: %s", hipGetErrorString(e));
     return H3A_OK;

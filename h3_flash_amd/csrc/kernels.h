@@ -35,6 +35,12 @@ int attn_fwd_block_m();
 int attn_fwd_row_margin();
 hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream);
 
+// n / d for 0 <= n < 2^31 as (umulhi(n, m) + n) >> s (Granlund-Montgomery).
+struct FastDiv {
+    uint32_t d, m, s;
+};
+FastDiv make_fast_div(uint32_t d);
+
 struct QkNormRopeParams {
     const void* x[2];
     void* y[2];
@@ -45,7 +51,8 @@ struct QkNormRopeParams {
     const float* cos;
     const float* sin;
     int64_t table_stride;
-    int64_t rows;  // batch * seqlen * n_tensors * heads
+    int64_t rows;  // batch * seqlen * n_tensors * heads, < 2^31
+    FastDiv div_heads, div_tensors, div_seqlen;
     int32_t seqlen;
     int32_t heads;
     int32_t n_tensors;  // 1 (q only) or 2 (q and k)

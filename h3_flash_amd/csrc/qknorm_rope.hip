@@ -10,17 +10,25 @@
 // s (fusions.py:141), so one cos/sin row serves every head of q and k.
 //
 // Layout: a row of D bf16 values is handled by L = D/8 lanes, 16 bytes each.
-// Rows are numbered (batch, token, tensor, head) with the head fastest, so the
-// 2*H rows of one token are processed by neighbouring lanes and read their
-// cos/sin row from HBM once. The kernel is HBM-bound: per token it moves
-// 2*H*D*2 bytes in, the same out, and 2*R*4 bytes of tables.
+// The kernel is HBM-bound: per token it moves 2*H*D*2 bytes in, the same out,
+// and 2*R*4 bytes of tables.
 #include "common.h"
 #include "kernels.h"
 
 namespace h3a {
+
+FastDiv make_fast_div(uint32_t d) {
+    uint32_t s = 0;
+    while (s < 32 && ((uint64_t)1 << s) < d) ++s;
+    const uint64_t m = (((uint64_t)1 << 32) * (((uint64_t)1 << s) - d)) / d + 1;
+    return FastDiv{d, (uint32_t)m, s};
+}
+
 namespace {
 
 constexpr int kThreads = 256;
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) { return (__umulhi(n, f.m) + n) >> f.s; }
 
 __device__ __forceinline__ void unpack8(i32x4 raw, float* f) {
 #pragma unroll
@@ -47,124 +55,184 @@ __device__ __forceinline__ void load_w8(const void* w, int col0, bool f32, float
     }
 }
 
-// L lanes per row; kFast: R % 16 == 0 and 16-byte aligned tables, so a lane's
-// 8 columns are either all rotary or all pass-through, its partner columns are
-// the 8 columns of lane (j +- R/16), and cos/sin come in two 16-byte loads.
-template <int L, bool kFast>
+struct RowRef {
+    const uint16_t* x;
+    uint16_t* y;
+    uint32_t s;
+    int which;
+    bool ok;
+};
+
+__device__ __forceinline__ RowRef locate(const QkNormRopeParams& p, uint32_t row) {
+    RowRef r;
+    r.ok = row < (uint32_t)p.rows;
+    const uint32_t rr = r.ok ? row : 0u;
+    const uint32_t t = fdiv(rr, p.div_heads);
+    const uint32_t h = rr - t * p.div_heads.d;
+    const uint32_t t2 = fdiv(t, p.div_tensors);
+    r.which = (int)(t - t2 * p.div_tensors.d);
+    const uint32_t b = fdiv(t2, p.div_seqlen);
+    r.s = t2 - b * p.div_seqlen.d;
+    const bool second = r.which != 0;
+    r.x = (const uint16_t*)(second ? p.x[1] : p.x[0]) + (int64_t)b * (second ? p.x_sb[1] : p.x_sb[0]) +
+          (int64_t)r.s * (second ? p.x_ss[1] : p.x_ss[0]) + (int64_t)h * (second ? p.x_sh[1] : p.x_sh[0]);
+    r.y = (uint16_t*)(second ? p.y[1] : p.y[0]) + (int64_t)b * (second ? p.y_sb[1] : p.y_sb[0]) +
+          (int64_t)r.s * (second ? p.y_ss[1] : p.y_ss[0]) + (int64_t)h * (second ? p.y_sh[1] : p.y_sh[0]);
+    return r;
+}
+
+// Fast path: R % 16 == 0 and 16-byte aligned tables, so a lane's 8 columns
+// are either all rotary or all pass-through, its partner columns are the 8
+// columns of lane (j +- R/16), and cos/sin come in two 16-byte loads.
+// One lane group per token: it reads the token's cos/sin once and walks the
+// token's rows tensor by tensor, kChunk heads at a time with all their loads
+// issued first; tensor and head are uniform over the block (scalar indexing).
+// Every byte of x and y is touched once: non-temporal accesses.
+template <int L>
 __global__ __launch_bounds__(kThreads) void qknorm_rope_kernel(QkNormRopeParams p) {
+    constexpr int kGroups = kThreads / L;
+    constexpr int kChunk = 8;
     const int tid = threadIdx.x;
-    const int64_t row = (int64_t)blockIdx.x * (kThreads / L) + tid / L;
     const int j = tid % L;
-    const int D = p.head_dim, R = p.rotary_dim, half = R >> 1;
-    // Lanes of a row past the end still join the shuffles below.
-    const bool row_ok = row < p.rows;
-    const int64_t rr = row_ok ? row : 0;
-    const int h = (int)(rr % p.heads);
-    int64_t t = rr / p.heads;
-    const int which = (int)(t % p.n_tensors);
-    t /= p.n_tensors;
-    const int s = (int)(t % p.seqlen);
-    const int64_t b = t / p.seqlen;
-
-    const uint16_t* x = (const uint16_t*)p.x[which] + b * p.x_sb[which] + s * p.x_ss[which] + h * p.x_sh[which];
-    uint16_t* y = (uint16_t*)p.y[which] + b * p.y_sb[which] + s * p.y_ss[which] + h * p.y_sh[which];
-    const void* w = p.w[which];
-    const bool wf = p.w_f32 != 0;
-
+    const int s = (int)blockIdx.x * kGroups + tid / L;  // token
+    const int64_t b = blockIdx.y;
+    const int D = p.head_dim, R = p.rotary_dim, half = R >> 1, H = p.heads;
     const int col0 = j * 8;
-    const bool active = row_ok && col0 < D;
-    float xv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (active) unpack8(*(const i32x4*)(x + col0), xv);
+    const bool on = s < p.seqlen && col0 < D;
+    const bool rot = col0 < R;
+    const bool first = col0 < half;
+    const int src = rot ? (first ? j + half / 8 : j - half / 8) : j;
+    const bool wf = p.w_f32 != 0;
+    const float inv_d = 1.0f / (float)D;
+    const bool d_pow2 = (D & (D - 1)) == 0;  // then ss * inv_d == ss / D exactly
 
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ss += xv[i] * xv[i];
-#pragma unroll
-    for (int off = L / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, L);
-    const float r = rsqrtf(ss / (float)D + p.eps[which]);
-
-    float out[8];
-    if constexpr (kFast) {
-        // Partner chunk lives in lane j +- R/16 of the same row.
-        const bool rot = col0 < R;
-        const bool first = col0 < half;
-        const int src = rot ? (first ? j + half / 8 : j - half / 8) : j;
-        uint32_t mine[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)  // re-pack the own chunk (exact: values came from bf16)
-            mine[i] = (__float_as_uint(xv[2 * i]) >> 16) | (__float_as_uint(xv[2 * i + 1]) & 0xffff0000u);
-        i32x4 praw;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) praw[i] = __shfl((int)mine[i], src, L);
-        float xp[8];
-        unpack8(praw, xp);
-        float wv[8];
-        if (active) load_w8(w, col0, wf, wv);
-        if (rot && active) {
-            float wp[8];
-            load_w8(w, src * 8, wf, wp);
-            const float* cp = p.cos + (int64_t)s * p.table_stride + col0;
-            const float* sp = p.sin + (int64_t)s * p.table_stride + col0;
-            const f32x4 c0 = *(const f32x4*)cp, c1 = *(const f32x4*)(cp + 4);
-            const f32x4 s0 = *(const f32x4*)sp, s1 = *(const f32x4*)(sp + 4);
-            const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
-            const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float n = xv[i] * r * wv[i];
-                const float pn = xp[i] * r * wp[i];
-                const float rt = first ? -pn : pn;
-                out[i] = n * cv[i] + rt * sv[i];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) out[i] = active ? xv[i] * r * wv[i] : 0.f;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int col = col0 + i;
-            float o = 0.f;
-            if (active && col < D) {
-                const float n = xv[i] * r * load_w(w, col, wf);
-                if (col < R) {
-                    const bool first = col < half;
-                    const int pc = first ? col + half : col - half;
-                    const float pn = bf16_to_f32(x[pc]) * r * load_w(w, pc, wf);
-                    const float rt = first ? -pn : pn;
-                    const float cv = p.cos[(int64_t)s * p.table_stride + col];
-                    const float sv = p.sin[(int64_t)s * p.table_stride + col];
-                    o = n * cv + rt * sv;
-                } else {
-                    o = n;
-                }
-            }
-            out[i] = o;
-        }
+    float cv[8], sv[8];
+    if (on && rot) {
+        const float* cp = p.cos + (int64_t)s * p.table_stride + col0;
+        const float* sp = p.sin + (int64_t)s * p.table_stride + col0;
+        const f32x4 c0 = *(const f32x4*)cp, c1 = *(const f32x4*)(cp + 4);
+        const f32x4 s0 = *(const f32x4*)sp, s1 = *(const f32x4*)(sp + 4);
+        cv[0] = c0.x; cv[1] = c0.y; cv[2] = c0.z; cv[3] = c0.w; cv[4] = c1.x; cv[5] = c1.y; cv[6] = c1.z; cv[7] = c1.w;
+        sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w; sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
     }
-    if (active) {
-        i32x4 packed;
+
+    for (int which = 0; which < p.n_tensors; ++which) {
+        const bool second = which != 0;
+        const void* w = second ? p.w[1] : p.w[0];
+        const float eps = second ? p.eps[1] : p.eps[0];
+        const int64_t xsh = second ? p.x_sh[1] : p.x_sh[0], ysh = second ? p.y_sh[1] : p.y_sh[0];
+        const uint16_t* xt = (const uint16_t*)(second ? p.x[1] : p.x[0]) + b * (second ? p.x_sb[1] : p.x_sb[0]) +
+                             (int64_t)s * (second ? p.x_ss[1] : p.x_ss[0]) + col0;
+        uint16_t* yt = (uint16_t*)(second ? p.y[1] : p.y[0]) + b * (second ? p.y_sb[1] : p.y_sb[0]) +
+                       (int64_t)s * (second ? p.y_ss[1] : p.y_ss[0]) + col0;
+        float wv[8], wp[8];
+        if (on) load_w8(w, col0, wf, wv);
+        if (on && rot) load_w8(w, src * 8, wf, wp);
+        for (int h0 = 0; h0 < H; h0 += kChunk) {
+            i32x4 raw[kChunk];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) packed[i] = (int)pack_bf16x2(out[2 * i], out[2 * i + 1]);
-        *(i32x4*)(y + col0) = packed;
+            for (int i = 0; i < kChunk; ++i) {
+                raw[i] = i32x4{0, 0, 0, 0};
+                if (h0 + i < H && on) raw[i] = __builtin_nontemporal_load((const i32x4*)(xt + (int64_t)(h0 + i) * xsh));
+            }
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i) {
+                if (h0 + i >= H) break;  // uniform
+                float xv[8];
+                unpack8(raw[i], xv);
+                float ss = 0.f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss += xv[e] * xv[e];
+#pragma unroll
+                for (int off = L / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, L);
+                const float r = rsqrtf((d_pow2 ? ss * inv_d : ss / (float)D) + eps);
+                // Partner chunk lives in lane src of the same row (all lanes join).
+                i32x4 praw;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) praw[e] = __shfl(raw[i][e], src, L);
+                if (!on) continue;
+                float out[8];
+                if (rot) {
+                    float xp[8];
+                    unpack8(praw, xp);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float n = xv[e] * r * wv[e];
+                        const float pn = xp[e] * r * wp[e];
+                        const float rt = first ? -pn : pn;
+                        out[e] = n * cv[e] + rt * sv[e];
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) out[e] = xv[e] * r * wv[e];
+                }
+                i32x4 packed;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) packed[e] = (int)pack_bf16x2(out[2 * e], out[2 * e + 1]);
+                __builtin_nontemporal_store(packed, (i32x4*)(yt + (int64_t)(h0 + i) * ysh));
+            }
+        }
     }
 }
 
-template <bool kFast>
-hipError_t launch_l(const QkNormRopeParams& p, hipStream_t stream) {
-    int lanes = 1;
-    while (lanes * 8 < p.head_dim) lanes <<= 1;
-    const int64_t rows_per_block = kThreads / lanes;
-    const unsigned blocks = (unsigned)((p.rows + rows_per_block - 1) / rows_per_block);
-    switch (lanes) {
-        case 1: hipLaunchKernelGGL((qknorm_rope_kernel<1, kFast>), dim3(blocks), dim3(kThreads), 0, stream, p); break;
-        case 2: hipLaunchKernelGGL((qknorm_rope_kernel<2, kFast>), dim3(blocks), dim3(kThreads), 0, stream, p); break;
-        case 4: hipLaunchKernelGGL((qknorm_rope_kernel<4, kFast>), dim3(blocks), dim3(kThreads), 0, stream, p); break;
-        case 8: hipLaunchKernelGGL((qknorm_rope_kernel<8, kFast>), dim3(blocks), dim3(kThreads), 0, stream, p); break;
-        case 16: hipLaunchKernelGGL((qknorm_rope_kernel<16, kFast>), dim3(blocks), dim3(kThreads), 0, stream, p); break;
-        case 32: hipLaunchKernelGGL((qknorm_rope_kernel<32, kFast>), dim3(blocks), dim3(kThreads), 0, stream, p); break;
-        case 64: hipLaunchKernelGGL((qknorm_rope_kernel<64, kFast>), dim3(blocks), dim3(kThreads), 0, stream, p); break;
-        default: return hipErrorInvalidValue;
+// Generic path (any even R <= D, any table alignment): one row per lane
+// group, element-wise partner and table reads.
+template <int L>
+__global__ __launch_bounds__(kThreads) void qknorm_rope_generic_kernel(QkNormRopeParams p) {
+    const int tid = threadIdx.x;
+    const int j = tid % L;
+    const RowRef ref = locate(p, blockIdx.x * (uint32_t)(kThreads / L) + (uint32_t)(tid / L));
+    const int D = p.head_dim, R = p.rotary_dim, half = R >> 1;
+    const int col0 = j * 8;
+    const bool active = ref.ok && col0 < D;
+    const void* w = ref.which ? p.w[1] : p.w[0];
+    const bool wf = p.w_f32 != 0;
+    float xv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (active) unpack8(*(const i32x4*)(ref.x + col0), xv);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += xv[e] * xv[e];
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, L);
+    if (!active) return;
+    const float r = rsqrtf(ss / (float)D + (ref.which ? p.eps[1] : p.eps[0]));
+    float out[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int col = col0 + e;
+        float o = 0.f;
+        if (col < D) {
+            const float n = xv[e] * r * load_w(w, col, wf);
+            if (col < R) {
+                const bool first = col < half;
+                const int pc = first ? col + half : col - half;
+                const float pn = bf16_to_f32(ref.x[pc]) * r * load_w(w, pc, wf);
+                const float rt = first ? -pn : pn;
+                const float cv = p.cos[(int64_t)ref.s * p.table_stride + col];
+                const float sv = p.sin[(int64_t)ref.s * p.table_stride + col];
+                o = n * cv + rt * sv;
+            } else {
+                o = n;
+            }
+        }
+        out[e] = o;
+    }
+    i32x4 packed;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) packed[e] = (int)pack_bf16x2(out[2 * e], out[2 * e + 1]);
+    *(i32x4*)(ref.y + col0) = packed;
+}
+
+template <int L>
+hipError_t launch_l(const QkNormRopeParams& p, bool fast, hipStream_t stream) {
+    if (fast) {
+        const int64_t batch = p.rows / ((int64_t)p.seqlen * p.n_tensors * p.heads);
+        const dim3 grid((unsigned)((p.seqlen + kThreads / L - 1) / (kThreads / L)), (unsigned)batch);
+        hipLaunchKernelGGL((qknorm_rope_kernel<L>), grid, dim3(kThreads), 0, stream, p);
+    } else {
+        const int64_t per_block = kThreads / L;
+        const unsigned blocks = (unsigned)((p.rows + per_block - 1) / per_block);
+        hipLaunchKernelGGL((qknorm_rope_generic_kernel<L>), dim3(blocks), dim3(kThreads), 0, stream, p);
     }
     return hipGetLastError();
 }
@@ -175,7 +243,18 @@ hipError_t launch_qknorm_rope(const QkNormRopeParams& p, hipStream_t stream) {
     if (p.rows <= 0) return hipSuccess;
     const bool aligned = ((uintptr_t)p.cos % 16 == 0) && ((uintptr_t)p.sin % 16 == 0) && (p.table_stride % 4 == 0);
     const bool fast = (p.rotary_dim % 16 == 0) && aligned;
-    return fast ? launch_l<true>(p, stream) : launch_l<false>(p, stream);
+    int lanes = 1;
+    while (lanes * 8 < p.head_dim) lanes <<= 1;
+    switch (lanes) {
+        case 1: return launch_l<1>(p, fast, stream);
+        case 2: return launch_l<2>(p, fast, stream);
+        case 4: return launch_l<4>(p, fast, stream);
+        case 8: return launch_l<8>(p, fast, stream);
+        case 16: return launch_l<16>(p, fast, stream);
+        case 32: return launch_l<32>(p, fast, stream);
+        case 64: return launch_l<64>(p, fast, stream);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace h3a

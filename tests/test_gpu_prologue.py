@@ -65,6 +65,19 @@ def test_widths_and_weight_dtypes(D, R, wdtype):
     assert_rounding_parity(y, qknorm_rope_reference(x, w, cos, sin, 1e-5), (D, R, wdtype))
 
 
+@pytest.mark.parametrize("H", [1, 8, 9, 40])
+def test_head_counts_around_the_chunk_size(H):
+    # heads are walked in chunks of 8 per token
+    B, S, D = 1, 50, 128
+    q, k = _rand((B, S, H, D), 30 + H), _rand((B, S, H, D), 60 + H)
+    wq = torch.randn(D, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16)
+    wk = torch.randn(D, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    cos, sin = rope_3d_tables((2, 5, 5))
+    oq, ok = fused_qk_norm_rope(q.to(DEV), k.to(DEV), wq.to(DEV), wk.to(DEV), cos.to(DEV), sin.to(DEV), 1e-5, 1e-6)
+    assert_rounding_parity(oq, qknorm_rope_reference(q, wq, cos, sin, 1e-5), ("q", H))
+    assert_rounding_parity(ok, qknorm_rope_reference(k, wk, cos, sin, 1e-6), ("k", H))
+
+
 def test_q_and_k_in_one_launch_equals_two_launches():
     B, S, H, D = 1, 300, 5, 128
     q, k = _rand((B, S, H, D), 1).to(DEV), _rand((B, S, H, D), 2).to(DEV)
