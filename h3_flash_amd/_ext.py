@@ -14,7 +14,7 @@ from pathlib import Path
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 H3A_OK = 0
 H3A_EINVAL = -1
@@ -52,6 +52,8 @@ class AttnArgs(ctypes.Structure):
         ("cu_seqlens_k", ctypes.c_void_p),
         ("num_segments", ctypes.c_int32),
         ("max_seqlen_q", ctypes.c_int32),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_int64),
     ]
 
 
@@ -85,6 +87,7 @@ class QkNormRopeArgs(ctypes.Structure):
 # Every function the header declares, with its ctypes signature.
 SIGNATURES = {
     "h3a_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
+    "h3a_attn_fwd_workspace_size": (ctypes.c_int64, [ctypes.POINTER(AttnArgs)]),
     "h3a_qknorm_rope": (ctypes.c_int, [ctypes.POINTER(QkNormRopeArgs), ctypes.c_void_p]),
     "h3a_last_error": (ctypes.c_char_p, []),
     "h3a_abi_version": (ctypes.c_int, []),

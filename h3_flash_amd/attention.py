@@ -80,6 +80,7 @@ def flash_attn_func(
     max_seqlen_q: int | None = None,
     out: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
+    split_tail: bool = True,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Non-causal attention forward on MI355X; returns ``(out, lse)``.
 
@@ -89,6 +90,11 @@ def flash_attn_func(
     ``num_segments + 1`` offsets into the sequence dimension, batch 1) the
     attention is block-diagonal over the packed segments. ``out``/``lse`` may
     be passed pre-allocated (BSHD bf16 / (B, H, Sq) fp32).
+
+    ``split_tail``: when the query tiles of a dense call leave the last round
+    of CUs partly idle, that round's tiles run as key-range pieces merged by
+    a second kernel; the workspace comes from torch's stream-ordered caching
+    allocator. ``False`` runs every tile whole (results differ by rounding).
 
     Raises RuntimeError for semantics the dense path does not serve (causal,
     GQA) and for a missing library, mirroring dense_fa4.py:19-20,72-73.
@@ -158,7 +164,14 @@ def flash_attn_func(
             lse.fill_(float("-inf"))
             return out, lse
     lib = _ext.load_library()
-    rc = lib.h3a_attn_fwd(ctypes.byref(args), ctypes.c_void_p(_stream_handle(q.device)))
+    workspace = None
+    with torch.cuda.device(q.device):
+        need = lib.h3a_attn_fwd_workspace_size(ctypes.byref(args)) if split_tail else 0
+        if need > 0:
+            # Stream-ordered caching allocation: reused, not freed, after the call.
+            workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+            args.workspace, args.workspace_bytes = workspace.data_ptr(), need
+        rc = lib.h3a_attn_fwd(ctypes.byref(args), ctypes.c_void_p(_stream_handle(q.device)))
     if rc != _ext.H3A_OK:
         message = _ext.last_error(lib)
         if rc == _ext.H3A_EINVAL:

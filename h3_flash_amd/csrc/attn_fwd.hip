@@ -100,14 +100,27 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     const int hi = lane >> 5;  // wave half
     const int l32 = lane & 31;
 
-    // Workgroups are dispatched round-robin over the 8 XCDs. Renumber them so
-    // that the workgroups resident on one XCD at the same time are
-    // consecutive query tiles of one head and share its K/V in that XCD's L2.
+    // Workgroups are dispatched round-robin over the 8 XCDs, workgroup i to
+    // XCD i % 8 as its (i / 8)-th. Renumber them so that the workgroups
+    // resident on one XCD at the same time are consecutive query tiles of one
+    // head and share its K/V in that XCD's L2. With a split, every XCD runs
+    // its share of whole tiles first and then its share of the pieces, so the
+    // pieces fill the last round evenly.
     const int nb = gridDim.x, bid = blockIdx.x;
     const int xcd = bid & 7, local = bid >> 3, per = nb >> 3, rem = nb & 7;
-    const int logical = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + local;
-    const int qt = logical % p.n_qtiles;
-    const int rest = logical / p.n_qtiles;
+    const int start = xcd * per + min(xcd, rem);  // first workgroup of this XCD's share
+    int tile = start + local, piece = -1;
+    if (p.split_n != 0) {
+        const int full_per = p.n_full >> 3;  // n_full is a multiple of 8
+        if (local < full_per) {
+            tile = xcd * full_per + local;
+        } else {
+            piece = start - xcd * full_per + (local - full_per);
+            tile = p.n_full + piece % p.split_tiles;
+        }
+    }
+    const int qt = tile % p.n_qtiles;
+    const int rest = tile / p.n_qtiles;
     const int h = rest % p.heads;
     const int grp = rest / p.heads;
 
@@ -123,6 +136,13 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     }
     const int m0 = qt * kBM;
     if (m0 >= sq) return;  // whole workgroup: tile beyond this segment
+    if (piece >= 0) {
+        // Piece c of split_n covers key tiles [c*n/split_n, (c+1)*n/split_n).
+        const int chunk = piece / p.split_tiles, nkt = (sk + kBN - 1) / kBN;
+        const int kt0 = chunk * nkt / p.split_n, kt1 = (chunk + 1) * nkt / p.split_n;
+        k0 += kt0 * kBN;
+        sk = min(sk - kt0 * kBN, (kt1 - kt0) * kBN);
+    }
 
     const char* qb = (const char*)p.q + 2 * (b * p.q_sb + h * p.q_sh) + (int64_t)q0 * p.q_rs;
     const char* kb = (const char*)p.k + 2 * (b * p.k_sb + h * p.k_sh) + (int64_t)k0 * p.k_rs;
@@ -509,6 +529,22 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         l_run = pr.x + pr.y;
     }
     const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
+    const float lse = l_run > 0.f ? (mc + __log2f(l_run)) * 0.69314718055994531f : -INFINITY;
+    if (piece >= 0) {
+        // Partial result of a key-range piece: normalised O and LSE in fp32.
+        const int row = wave * 32 + l32;
+        float* wo = p.ws_o + ((int64_t)piece * kBM + row) * kD;
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int d = db * 32 + i * 8 + hi * 4;
+                *(f32x4*)(wo + d) = f32x4{oacc[db][i * 4 + 0] * inv, oacc[db][i * 4 + 1] * inv,
+                                          oacc[db][i * 4 + 2] * inv, oacc[db][i * 4 + 3] * inv};
+            }
+        if (hi == 0) p.ws_lse[(int64_t)piece * kBM + row] = lse;
+        return;
+    }
     if (mq < sq) {
         char* ob = (char*)p.o + 2 * (b * p.o_sb + h * p.o_sh) + (int64_t)(q0 + mq) * p.o_rs;
 #pragma unroll
@@ -521,22 +557,102 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
                 w.y = (int)pack_bf16x2(oacc[db][i * 4 + 2] * inv, oacc[db][i * 4 + 3] * inv);
                 *(i32x2*)(ob + d * 2) = w;
             }
-        if (p.lse != nullptr && hi == 0) {
-            const float lse = l_run > 0.f ? (mc + __log2f(l_run)) * 0.69314718055994531f : -INFINITY;
-            p.lse[b * p.lse_sb + h * p.lse_sh + q0 + mq] = lse;
+        if (p.lse != nullptr && hi == 0) p.lse[b * p.lse_sb + h * p.lse_sh + q0 + mq] = lse;
+    }
+}
+
+// Combines the split_n partial results of each split tile: with weights
+// w_i = exp(lse_i - max lse), O = sum w_i O_i / sum w_i and
+// LSE = max lse + log(sum w_i). 32 rows per workgroup, 8 lanes per row,
+// 16 head dims per lane.
+constexpr int kMergeRows = 32;
+
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
+    const int split_tile = blockIdx.x / (kBM / kMergeRows);
+    const int row = (blockIdx.x % (kBM / kMergeRows)) * kMergeRows + threadIdx.x / 8;
+    const int d0 = (threadIdx.x % 8) * 16;
+    const int tile = p.n_full + split_tile;
+    const int qt = tile % p.n_qtiles;
+    const int rest = tile / p.n_qtiles;
+    const int h = rest % p.heads;
+    const int b = rest / p.heads;
+    const int mq = qt * kBM + row;
+    if (mq >= p.seqlen_q) return;
+    float lse_max = -INFINITY;
+    for (int c = 0; c < p.split_n; ++c)
+        lse_max = fmaxf(lse_max, p.ws_lse[((int64_t)c * p.split_tiles + split_tile) * kBM + row]);
+    f32x4 acc[4] = {f32x4{}, f32x4{}, f32x4{}, f32x4{}};
+    float wsum = 0.f;
+    if (lse_max != -INFINITY) {
+        for (int c = 0; c < p.split_n; ++c) {
+            const int64_t pc = (int64_t)c * p.split_tiles + split_tile;
+            const float w = __expf(p.ws_lse[pc * kBM + row] - lse_max);
+            wsum += w;
+            const f32x4* src = (const f32x4*)(p.ws_o + (pc * kBM + row) * kD + d0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += w * src[i];
         }
     }
+    const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
+    char* ob = (char*)p.o + 2 * (b * p.o_sb + h * p.o_sh + d0) + (int64_t)mq * p.o_rs;
+    i32x4 w0, w1;
+    w0.x = (int)pack_bf16x2(acc[0].x * inv, acc[0].y * inv);
+    w0.y = (int)pack_bf16x2(acc[0].z * inv, acc[0].w * inv);
+    w0.z = (int)pack_bf16x2(acc[1].x * inv, acc[1].y * inv);
+    w0.w = (int)pack_bf16x2(acc[1].z * inv, acc[1].w * inv);
+    w1.x = (int)pack_bf16x2(acc[2].x * inv, acc[2].y * inv);
+    w1.y = (int)pack_bf16x2(acc[2].z * inv, acc[2].w * inv);
+    w1.z = (int)pack_bf16x2(acc[3].x * inv, acc[3].y * inv);
+    w1.w = (int)pack_bf16x2(acc[3].z * inv, acc[3].w * inv);
+    *(i32x4*)ob = w0;
+    *(i32x4*)(ob + 16) = w1;
+    if (p.lse != nullptr && d0 == 0)
+        p.lse[b * p.lse_sb + h * p.lse_sh + mq] = wsum > 0.f ? lse_max + __logf(wsum) : -INFINITY;
 }
 
 }  // namespace
 
 int attn_fwd_block_m() { return kBM; }
+int attn_fwd_block_n() { return kBN; }
 int attn_fwd_row_margin() { return kBM + kBN * (2 * kStages + 2); }
 
+SplitPlan plan_attn_split(int64_t tiles, int64_t key_tiles, int cus) {
+    // Whole rounds of tiles run as they are; the tiles of a partial last
+    // round are cut into n key-range pieces when that shortens the round
+    // (n <= 8, at least one key tile per piece): ceil(rest * n / cus) / n.
+    // The chip is power-bound under this kernel: a last round that keeps 70%
+    // or more of the CUs busy runs at a higher clock and loses little, and
+    // splitting it does not pay for the pieces and the merge.
+    SplitPlan plan{(int32_t)tiles, 0, 0, 0};
+    if (cus < 8 || cus % 8 != 0 || tiles <= 0) return plan;
+    const int64_t full = tiles / cus * cus, rest = tiles - full;
+    if (rest == 0 || rest * 10 >= (int64_t)cus * 7) return plan;
+    double best = 1.0;
+    int best_n = 0;
+    for (int n = 2; n <= 8 && n <= key_tiles; ++n) {
+        const double cost = (double)((rest * n + cus - 1) / cus) / n;
+        if (cost < best - 0.05) {
+            best = cost;
+            best_n = n;
+        }
+    }
+    if (best_n == 0) return plan;
+    plan.n_full = (int32_t)full;
+    plan.split_n = best_n;
+    plan.split_tiles = (int32_t)rest;
+    plan.workspace_bytes = (int64_t)best_n * rest * kBM * (kD + 1) * (int64_t)sizeof(float);
+    return plan;
+}
+
 hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
-    const int64_t blocks = (int64_t)p.n_qtiles * p.heads * p.n_groups;
-    if (blocks <= 0) return hipSuccess;
+    const int64_t tiles = (int64_t)p.n_qtiles * p.heads * p.n_groups;
+    if (tiles <= 0) return hipSuccess;
+    const int64_t blocks = p.split_n ? (int64_t)p.n_full + (int64_t)p.split_n * p.split_tiles : tiles;
     hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.split_n == 0) return e;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(p.split_tiles * (kBM / kMergeRows))), dim3(256), 0, stream,
+                       p);
     return hipGetLastError();
 }
 

@@ -1,9 +1,12 @@
 // extern "C" entry points declared in include/h3attn.h: argument validation,
 // error reporting and launch of the gfx950 kernels. No allocation, no host
-// synchronisation, no global mutable state besides the per-thread message.
+// synchronisation, no global mutable state besides the per-thread message and
+// a per-device cache of the CU count.
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+
+#include <atomic>
 
 #include "h3attn.h"
 #include "kernels.h"
@@ -24,16 +27,10 @@ constexpr int64_t kMaxSpan = (int64_t)1 << 31;  // buffer offsets are 32-bit
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-}  // namespace
-
-extern "C" {
-
-const char* h3a_last_error(void) { return g_err; }
-
-int h3a_abi_version(void) { return H3A_ABI_VERSION; }
-
-int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
-    g_err[0] = '\0';
+// Validates the arguments and fills the launch description (split off);
+// *empty: nothing to launch.
+int prepare_attn(const h3a_attn_args* a, h3a::AttnParams& p, bool* empty) {
+    *empty = false;
     if (a == nullptr) return fail(H3A_EINVAL, "h3a_attn_fwd: args is NULL");
     if (a->abi_version != H3A_ABI_VERSION)
         return fail(H3A_EINVAL, "h3a_attn_fwd: abi_version %d, library is %d", a->abi_version, H3A_ABI_VERSION);
@@ -44,7 +41,10 @@ int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
                     (long long)a->batch, (long long)a->heads, (long long)a->seqlen_q, (long long)a->seqlen_k);
     if (!(a->softmax_scale > 0.f) || !isfinite(a->softmax_scale))
         return fail(H3A_EINVAL, "h3a_attn_fwd: softmax_scale must be finite and > 0");
-    if (a->batch == 0 || a->seqlen_q == 0) return H3A_OK;
+    if (a->batch == 0 || a->seqlen_q == 0) {
+        *empty = true;
+        return H3A_OK;
+    }
     if (!a->q || !a->o || (a->seqlen_k > 0 && (!a->k || !a->v)))
         return fail(H3A_EINVAL, "h3a_attn_fwd: NULL tensor pointer");
     if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))
@@ -60,7 +60,6 @@ int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
 
     const bool varlen = a->cu_seqlens_q != nullptr;
     int64_t rows_q = a->seqlen_q, rows_k = a->seqlen_k;
-    h3a::AttnParams p{};
     p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o; p.lse = a->lse;
     p.q_sb = a->q_stride[0]; p.q_sh = a->q_stride[2];
     p.k_sb = a->k_stride[0]; p.k_sh = a->k_stride[2];
@@ -108,9 +107,69 @@ int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
     p.o_rs = (int32_t)(a->o_stride[1] * 2);
     const int64_t blocks = (int64_t)p.n_qtiles * p.heads * p.n_groups;
     if (blocks > INT32_MAX) return fail(H3A_EUNSUPPORTED, "h3a_attn_fwd: grid too large");
+    return H3A_OK;
+}
+
+// CU count of the current device, cached per device.
+int device_cus() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < 64) {
+        const int c = cache[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+    return n;
+}
+
+// Split plan of a validated launch: dense inputs only (varlen tiles are not
+// uniform work).
+h3a::SplitPlan attn_plan(const h3a_attn_args* a, const h3a::AttnParams& p) {
+    const int64_t tiles = (int64_t)p.n_qtiles * p.heads * p.n_groups;
+    h3a::SplitPlan none{(int32_t)tiles, 0, 0, 0};
+    if (a->cu_seqlens_q != nullptr) return none;
+    const int bn = h3a::attn_fwd_block_n();
+    return h3a::plan_attn_split(tiles, (a->seqlen_k + bn - 1) / bn, device_cus());
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* h3a_last_error(void) { return g_err; }
+
+int h3a_abi_version(void) { return H3A_ABI_VERSION; }
+
+int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
+    g_err[0] = '\0';
+    h3a::AttnParams p{};
+    bool empty = false;
+    const int rc = prepare_attn(a, p, &empty);
+    if (rc != H3A_OK || empty) return rc;
+    const h3a::SplitPlan plan = attn_plan(a, p);
+    if (plan.split_n != 0 && a->workspace != nullptr && a->workspace_bytes >= plan.workspace_bytes &&
+        ((uintptr_t)a->workspace & 255u) == 0) {
+        p.n_full = plan.n_full;
+        p.split_n = plan.split_n;
+        p.split_tiles = plan.split_tiles;
+        p.ws_o = (float*)a->workspace;
+        p.ws_lse = p.ws_o + (int64_t)plan.split_n * plan.split_tiles * h3a::attn_fwd_block_m() * 128;
+    }
     hipError_t e = h3a::launch_attn_fwd(p, (hipStream_t)stream);
     if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_attn_fwd: launch failed: %s", hipGetErrorString(e));
     return H3A_OK;
+}
+
+int64_t h3a_attn_fwd_workspace_size(const h3a_attn_args* a) {
+    g_err[0] = '\0';
+    h3a::AttnParams p{};
+    bool empty = false;
+    const int rc = prepare_attn(a, p, &empty);
+    if (rc != H3A_OK) return rc;
+    return empty ? 0 : attn_plan(a, p).workspace_bytes;
 }
 
 int h3a_qknorm_rope(const h3a_qknorm_rope_args* a, void* stream) {

@@ -27,9 +27,26 @@ struct AttnParams {
     float scale_log2;  // softmax_scale * log2(e)
     const int32_t* cu_q;  // NULL for dense
     const int32_t* cu_k;
+    // Key-range split of the last tiles (dense only; split_n == 0: none).
+    // Tiles [0, n_full) run whole; tiles [n_full, n_full + split_tiles) run as
+    // split_n pieces each, which write normalised fp32 partial O and LSE to
+    // ws_o / ws_lse for attn_merge to combine.
+    int32_t n_full;
+    int32_t split_n;
+    int32_t split_tiles;
+    float* ws_o;    // [split_n * split_tiles][kBM][128]
+    float* ws_lse;  // [split_n * split_tiles][kBM]
 };
 
+// How the query tiles of a dense launch are spread over the CUs.
+struct SplitPlan {
+    int32_t n_full, split_n, split_tiles;
+    int64_t workspace_bytes;
+};
+SplitPlan plan_attn_split(int64_t tiles, int64_t key_tiles, int cus);
+
 int attn_fwd_block_m();
+int attn_fwd_block_n();
 // Rows past the end of a sequence that the kernel may address (all reads there
 // are bounds-checked buffer loads returning zero).
 int attn_fwd_row_margin();

@@ -18,7 +18,8 @@
  *
  * Conventions
  *   - All tensor pointers are device pointers allocated by the caller; the
- *     library allocates nothing and keeps no per-call state.
+ *     library allocates nothing and keeps no per-call state (an attention
+ *     workspace, when used, is caller memory too).
  *   - Strides are in elements. The last (head_dim / rotary) dimension must be
  *     contiguous.
  *   - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream).
@@ -40,7 +41,7 @@ extern "C" {
 /* The library is built with hidden visibility; only these symbols export. */
 #define H3A_API __attribute__((visibility("default")))
 
-#define H3A_ABI_VERSION 1
+#define H3A_ABI_VERSION 2
 
 #define H3A_OK 0
 #define H3A_EINVAL (-1)       /* invalid argument (shape, stride, pointer) */
@@ -68,6 +69,14 @@ extern "C" {
  * block-diagonal: a query attends only to keys of its own segment.
  *
  * Rows with no key (seqlen_k == 0) produce O = 0 and LSE = -inf.
+ *
+ * Workspace (dense inputs only): when the query tiles do not fill the GPU's
+ * CUs in whole rounds, the tiles of the partial last round run as several
+ * key-range pieces whose fp32 partial results are merged by a second kernel
+ * on the same stream. That needs h3a_attn_fwd_workspace_size(args) bytes of
+ * device memory at `workspace` (256-byte aligned); with a NULL or smaller
+ * workspace every tile runs whole. The results differ only by rounding.
+ * Calls sharing one workspace must be ordered (same stream).
  */
 typedef struct h3a_attn_args {
     int32_t abi_version; /* must be H3A_ABI_VERSION */
@@ -92,9 +101,18 @@ typedef struct h3a_attn_args {
     const int32_t *cu_seqlens_k;
     int32_t num_segments;
     int32_t max_seqlen_q;
+    void *workspace;         /* device memory or NULL, see above */
+    int64_t workspace_bytes; /* bytes available at workspace */
 } h3a_attn_args;
 
 H3A_API int h3a_attn_fwd(const h3a_attn_args *args, void *stream);
+
+/*
+ * Bytes of workspace h3a_attn_fwd can use for these arguments on the current
+ * device (0: none); a negative H3A_E* code when the arguments are invalid.
+ * No counterpart in the reference: FlashAttention sizes its own scratch.
+ */
+H3A_API int64_t h3a_attn_fwd_workspace_size(const h3a_attn_args *args);
 
 /*
  * Fused per-head RMSNorm + rotate-half RoPE on q and k in one launch:

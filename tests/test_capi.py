@@ -32,7 +32,13 @@ def lib():
 
 
 def test_header_declares_the_expected_entry_points():
-    assert declared_functions() == ["h3a_abi_version", "h3a_attn_fwd", "h3a_last_error", "h3a_qknorm_rope"]
+    assert declared_functions() == [
+        "h3a_abi_version",
+        "h3a_attn_fwd",
+        "h3a_attn_fwd_workspace_size",
+        "h3a_last_error",
+        "h3a_qknorm_rope",
+    ]
 
 
 def test_library_exports_every_declared_function(lib):
@@ -42,7 +48,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_abi_version(lib):
-    assert lib.h3a_abi_version() == _ext.ABI_VERSION == 1
+    assert lib.h3a_abi_version() == _ext.ABI_VERSION == 2
 
 
 def _attn_args(**overrides):
@@ -103,6 +109,14 @@ def test_attn_null_args_and_empty_problem(lib):
     assert lib.h3a_attn_fwd(ctypes.byref(_attn_args(seqlen_q=0)), None) == _ext.H3A_OK
     assert lib.h3a_attn_fwd(ctypes.byref(_attn_args(batch=0)), None) == _ext.H3A_OK
     assert _ext.last_error(lib) == ""
+
+
+def test_workspace_size_validates_like_the_launch(lib):
+    # host-only call: no device work whether or not a GPU is visible
+    assert lib.h3a_attn_fwd_workspace_size(None) == _ext.H3A_EINVAL
+    assert lib.h3a_attn_fwd_workspace_size(ctypes.byref(_attn_args(head_dim=64))) == _ext.H3A_EUNSUPPORTED
+    assert lib.h3a_attn_fwd_workspace_size(ctypes.byref(_attn_args(seqlen_q=0))) == 0
+    assert lib.h3a_attn_fwd_workspace_size(ctypes.byref(_attn_args())) >= 0
 
 
 def _rope_args(**overrides):

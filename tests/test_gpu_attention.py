@@ -170,6 +170,49 @@ def test_score_jump_past_exponent_range():
         assert_parity(out, lse, ref_o, ref_l, ("jump", pos))
 
 
+def test_split_tail_matches_whole_tiles():
+    # on a 256-CU part: c1 (64 tiles) runs every tile as 4 key-range pieces,
+    # the 3-batch shape (84 tiles, ragged key range) as 3 pieces
+    for shape in ((1, 4096, 4096, 4), (3, 1000, 3000, 7)):
+        B, Sq, Sk, H = shape
+        q, k, v = (_rand(s_, 40 + i).to(DEV) for i, s_ in enumerate(((B, Sq, H, 128), (B, Sk, H, 128), (B, Sk, H, 128))))
+        o1, l1 = flash_attn_func(q, k, v)
+        o0, l0 = flash_attn_func(q, k, v, split_tail=False)
+        torch.cuda.synchronize()
+        assert (o1.float() - o0.float()).abs().max().item() <= 8e-3, shape
+        assert (l1 - l0).abs().max().item() <= 1e-5, shape
+        ref_o, ref_l = sdpa_reference(q.cpu(), k.cpu(), v.cpu())
+        assert_parity(o1.cpu(), l1.cpu(), ref_o, ref_l, ("split", shape))
+
+
+def test_workspace_plan_on_this_device():
+    import ctypes
+
+    from h3_flash_amd import _ext
+
+    lib = _ext.load_library()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+
+    def need(B, S, H):
+        a = _ext.AttnArgs()
+        a.abi_version = _ext.ABI_VERSION
+        a.q = a.k = a.v = a.o = 1 << 20
+        a.batch, a.heads, a.seqlen_q, a.seqlen_k, a.head_dim = B, H, S, S, 128
+        for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+            getattr(a, name)[:] = (S * H * 128, H * 128, 128)
+        a.lse_stride[:] = (H * S, S)
+        a.softmax_scale = 0.088
+        return lib.h3a_attn_fwd_workspace_size(ctypes.byref(a))
+
+    per_piece = 256 * 129 * 4
+    if cus == 256:
+        assert need(1, 49920, 5) == 0  # 975 tiles: last round 81% full, not split
+        assert need(1, 4096, 4) == 4 * 64 * per_piece  # 64 tiles, 4 pieces each
+        assert need(1, 256 * 40, 36) == 3 * 160 * per_piece  # 1440 tiles: 1280 whole, 160 in 3 pieces
+        assert need(1, 256 * 128, 8) == 0  # 1024 tiles: whole rounds
+    assert need(1, 64, 1) == 0  # one key tile: nothing to split
+
+
 def test_unsupported_requests_raise():
     q = _rand((1, 8, 2, 128), 15).to(DEV)
     with pytest.raises(RuntimeError, match="non-causal"):
@@ -227,7 +270,9 @@ def test_c5_packed_varlen_sampled_rows():
     assert_parity(out[:, rows.to(DEV)].cpu(), lse[:, :, rows.to(DEV)].cpu(), ref_o, ref_l, "c5")
     # the audio segment must not see video keys: compare with a standalone run
     a0 = 49920
-    oa_, la_ = flash_attn_func(q[:, a0:].contiguous(), k[:, a0:].contiguous(), v[:, a0:].contiguous())
+    oa_, la_ = flash_attn_func(
+        q[:, a0:].contiguous(), k[:, a0:].contiguous(), v[:, a0:].contiguous(), split_tail=False
+    )
     torch.cuda.synchronize()
     assert torch.equal(oa_, out[:, a0:]) and torch.equal(la_, lse[:, :, a0:])
 
