@@ -14,7 +14,7 @@ from pathlib import Path
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 H3A_OK = 0
 H3A_EINVAL = -1
@@ -84,11 +84,71 @@ class QkNormRopeArgs(ctypes.Structure):
     ]
 
 
+class PackQkvArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("elem_bytes", ctypes.c_int64),
+        ("rows", ctypes.c_int64),
+        ("heads", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("world", ctypes.c_int64),
+        ("q_stride", _I64x2),
+        ("k_stride", _I64x2),
+        ("v_stride", _I64x2),
+    ]
+
+
+class MergeHeadsArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("x", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("elem_bytes", ctypes.c_int64),
+        ("world", ctypes.c_int64),
+        ("rows", ctypes.c_int64),
+        ("inner", ctypes.c_int64),
+        ("x_stride", _I64x2),
+    ]
+
+
+class QkNormRopePackArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("q", ctypes.c_void_p),
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("wq", ctypes.c_void_p),
+        ("wk", ctypes.c_void_p),
+        ("w_dtype", ctypes.c_int32),
+        ("cos", ctypes.c_void_p),
+        ("sin", ctypes.c_void_p),
+        ("table_stride", ctypes.c_int64),
+        ("rows", ctypes.c_int64),
+        ("heads", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("rotary_dim", ctypes.c_int64),
+        ("world", ctypes.c_int64),
+        ("q_stride", _I64x2),
+        ("k_stride", _I64x2),
+        ("v_stride", _I64x2),
+        ("eps_q", ctypes.c_float),
+        ("eps_k", ctypes.c_float),
+    ]
+
+
 # Every function the header declares, with its ctypes signature.
 SIGNATURES = {
     "h3a_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
     "h3a_attn_fwd_workspace_size": (ctypes.c_int64, [ctypes.POINTER(AttnArgs)]),
     "h3a_qknorm_rope": (ctypes.c_int, [ctypes.POINTER(QkNormRopeArgs), ctypes.c_void_p]),
+    "h3a_pack_qkv": (ctypes.c_int, [ctypes.POINTER(PackQkvArgs), ctypes.c_void_p]),
+    "h3a_merge_heads": (ctypes.c_int, [ctypes.POINTER(MergeHeadsArgs), ctypes.c_void_p]),
+    "h3a_qknorm_rope_pack": (ctypes.c_int, [ctypes.POINTER(QkNormRopePackArgs), ctypes.c_void_p]),
     "h3a_last_error": (ctypes.c_char_p, []),
     "h3a_abi_version": (ctypes.c_int, []),
 }

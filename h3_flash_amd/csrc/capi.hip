@@ -226,8 +226,157 @@ int h3a_qknorm_rope(const h3a_qknorm_rope_args* a, void* stream) {
     p.div_heads = h3a::make_fast_div((uint32_t)a->heads);
     p.div_tensors = h3a::make_fast_div((uint32_t)n);
     p.div_seqlen = h3a::make_fast_div((uint32_t)a->seqlen);
+    p.div_hpg = p.div_heads;  // ungrouped output heads
     hipError_t e = h3a::launch_qknorm_rope(p, (hipStream_t)stream);
     if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_qknorm_rope: launch failed: %s", hipGetErrorString(e));
+    return H3A_OK;
+}
+
+int h3a_pack_qkv(const h3a_pack_qkv_args* a, void* stream) {
+    g_err[0] = '\0';
+    if (a == nullptr) return fail(H3A_EINVAL, "h3a_pack_qkv: args is NULL");
+    if (a->abi_version != H3A_ABI_VERSION)
+        return fail(H3A_EINVAL, "h3a_pack_qkv: abi_version %d, library is %d", a->abi_version, H3A_ABI_VERSION);
+    const int64_t es = a->elem_bytes;
+    if (es != 1 && es != 2 && es != 4 && es != 8)
+        return fail(H3A_EINVAL, "h3a_pack_qkv: elem_bytes must be 1, 2, 4 or 8, got %lld", (long long)es);
+    if (a->rows < 0 || a->heads <= 0 || a->head_dim <= 0 || a->world <= 0)
+        return fail(H3A_EINVAL, "h3a_pack_qkv: bad extents (rows=%lld heads=%lld head_dim=%lld world=%lld)",
+                    (long long)a->rows, (long long)a->heads, (long long)a->head_dim, (long long)a->world);
+    if (a->heads % a->world != 0)
+        return fail(H3A_EINVAL, "heads (%lld) must divide Ulysses degree (%lld)", (long long)a->heads,
+                    (long long)a->world);
+    if (a->rows == 0) return H3A_OK;
+    if (!a->q || !a->k || !a->v || !a->out) return fail(H3A_EINVAL, "h3a_pack_qkv: NULL tensor pointer");
+    const int64_t* st[3] = {a->q_stride, a->k_stride, a->v_stride};
+    const void* src[3] = {a->q, a->k, a->v};
+    const int64_t row_bytes = a->head_dim * es;
+    if (a->rows * a->heads >= ((int64_t)1 << 31) || row_bytes >= ((int64_t)1 << 30))
+        return fail(H3A_EUNSUPPORTED, "h3a_pack_qkv: %lld (row, head) units of %lld bytes (limits 2^31, 2^30)",
+                    (long long)(a->rows * a->heads), (long long)row_bytes);
+    h3a::PackQkvParams p{};
+    bool vec = row_bytes % 16 == 0 && row_bytes <= 4096 && aligned16(a->out);
+    for (int i = 0; i < 3; ++i) {
+        if (st[i][0] < 0 || st[i][1] < 0) return fail(H3A_EINVAL, "h3a_pack_qkv: strides must be non-negative");
+        p.src[i] = src[i];
+        p.s_row[i] = st[i][0] * es;
+        p.s_head[i] = st[i][1] * es;
+        vec = vec && aligned16(src[i]) && p.s_row[i] % 16 == 0 && p.s_head[i] % 16 == 0;
+    }
+    p.out = a->out;
+    p.rows = a->rows;
+    p.row_bytes = (int32_t)row_bytes;
+    p.units = (uint32_t)(a->rows * a->heads);
+    p.div_heads = h3a::make_fast_div((uint32_t)a->heads);
+    p.div_hl = h3a::make_fast_div((uint32_t)(a->heads / a->world));
+    hipError_t e = h3a::launch_pack_qkv(p, vec, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_pack_qkv: launch failed: %s", hipGetErrorString(e));
+    return H3A_OK;
+}
+
+int h3a_merge_heads(const h3a_merge_heads_args* a, void* stream) {
+    g_err[0] = '\0';
+    if (a == nullptr) return fail(H3A_EINVAL, "h3a_merge_heads: args is NULL");
+    if (a->abi_version != H3A_ABI_VERSION)
+        return fail(H3A_EINVAL, "h3a_merge_heads: abi_version %d, library is %d", a->abi_version, H3A_ABI_VERSION);
+    const int64_t es = a->elem_bytes;
+    if (es != 1 && es != 2 && es != 4 && es != 8)
+        return fail(H3A_EINVAL, "h3a_merge_heads: elem_bytes must be 1, 2, 4 or 8, got %lld", (long long)es);
+    if (a->world <= 0 || a->rows < 0 || a->inner < 0)
+        return fail(H3A_EINVAL, "h3a_merge_heads: bad extents (world=%lld rows=%lld inner=%lld)", (long long)a->world,
+                    (long long)a->rows, (long long)a->inner);
+    if (a->x_stride[0] < 0 || a->x_stride[1] < 0) return fail(H3A_EINVAL, "h3a_merge_heads: strides must be non-negative");
+    if (a->rows == 0 || a->inner == 0) return H3A_OK;
+    if (!a->x || !a->out) return fail(H3A_EINVAL, "h3a_merge_heads: NULL tensor pointer");
+    if (a->world >= ((int64_t)1 << 31)) return fail(H3A_EUNSUPPORTED, "h3a_merge_heads: world too large");
+    h3a::MergeHeadsParams p{};
+    p.x = a->x;
+    p.out = a->out;
+    p.s_world = a->x_stride[0] * es;
+    p.s_row = a->x_stride[1] * es;
+    p.rows = a->rows;
+    p.inner_bytes = a->inner * es;
+    const int64_t vectors = a->rows * a->world * (p.inner_bytes / 16);
+    const bool vec = p.inner_bytes % 16 == 0 && aligned16(a->x) && aligned16(a->out) && p.s_world % 16 == 0 &&
+                     p.s_row % 16 == 0 && vectors < ((int64_t)1 << 31);
+    if (vec) {
+        p.vectors = (uint32_t)vectors;
+        p.div_inner = h3a::make_fast_div((uint32_t)(p.inner_bytes / 16));
+    }
+    p.div_world = h3a::make_fast_div((uint32_t)a->world);
+    hipError_t e = h3a::launch_merge_heads(p, vec, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_merge_heads: launch failed: %s", hipGetErrorString(e));
+    return H3A_OK;
+}
+
+int h3a_qknorm_rope_pack(const h3a_qknorm_rope_pack_args* a, void* stream) {
+    g_err[0] = '\0';
+    if (a == nullptr) return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: args is NULL");
+    if (a->abi_version != H3A_ABI_VERSION)
+        return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: abi_version %d, library is %d", a->abi_version, H3A_ABI_VERSION);
+    const int64_t D = a->head_dim, R = a->rotary_dim;
+    if (R > D || R % 2 != 0 || R < 0)
+        return fail(H3A_EINVAL,
+                    "fused qknorm+rope requires an even rotary dimension no wider than the head, got rotary_dim=%lld, "
+                    "head_dim=%lld",
+                    (long long)R, (long long)D);
+    if (D <= 0 || D % 8 != 0 || D > 512)
+        return fail(H3A_EUNSUPPORTED, "h3a_qknorm_rope_pack: head_dim must be a multiple of 8 in [8, 512], got %lld",
+                    (long long)D);
+    if (a->rows < 0 || a->heads <= 0 || a->world <= 0)
+        return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: bad extents");
+    if (a->heads % a->world != 0)
+        return fail(H3A_EINVAL, "heads (%lld) must divide Ulysses degree (%lld)", (long long)a->heads,
+                    (long long)a->world);
+    if (a->w_dtype != H3A_DTYPE_BF16 && a->w_dtype != H3A_DTYPE_F32)
+        return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: unknown weight dtype %d", a->w_dtype);
+    if (a->rows == 0) return H3A_OK;
+    if (!a->q || !a->k || !a->v || !a->out || !a->wq || !a->wk)
+        return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: NULL tensor pointer");
+    if (R > 0 && (!a->cos || !a->sin)) return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: NULL cos/sin table");
+    if (R > 0 && a->table_stride < R) return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: table_stride < rotary_dim");
+    const void* ptrs[6] = {a->q, a->k, a->v, a->out, a->wq, a->wk};
+    for (const void* q : ptrs)
+        if (!aligned16(q)) return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: tensors must be 16-byte aligned");
+    const int64_t* st[3] = {a->q_stride, a->k_stride, a->v_stride};
+    for (int i = 0; i < 3; ++i)
+        for (int d = 0; d < 2; ++d)
+            if (st[i][d] < 0 || st[i][d] % 8 != 0)
+                return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: strides must be non-negative multiples of 8 elements");
+    if (a->rows * 2 * a->heads >= ((int64_t)1 << 31))
+        return fail(H3A_EUNSUPPORTED, "h3a_qknorm_rope_pack: %lld rows (limit 2^31 / (2 * heads))", (long long)a->rows);
+    const int64_t hl = a->heads / a->world;
+    const int64_t slot = 3 * D;         // one head's q|k|v in the packed buffer
+    const int64_t row_stride = hl * slot;  // one row of one destination
+    const int64_t group_stride = a->rows * row_stride;  // one destination
+    uint16_t* out = (uint16_t*)a->out;
+    h3a::QkNormRopeParams p{};
+    p.x[0] = a->q; p.x[1] = a->k;
+    p.y[0] = out; p.y[1] = out + D;
+    p.w[0] = a->wq; p.w[1] = a->wk;
+    p.eps[0] = a->eps_q; p.eps[1] = a->eps_k;
+    for (int i = 0; i < 2; ++i) {
+        p.x_sb[i] = 0; p.x_ss[i] = st[i][0]; p.x_sh[i] = st[i][1];
+        p.y_sb[i] = 0; p.y_ss[i] = row_stride; p.y_sh[i] = slot; p.y_sg[i] = group_stride;
+    }
+    p.xc = a->v; p.yc = out + 2 * D;
+    p.xc_sb = 0; p.xc_ss = a->v_stride[0]; p.xc_sh = a->v_stride[1];
+    p.yc_sb = 0; p.yc_ss = row_stride; p.yc_sh = slot; p.yc_sg = group_stride;
+    p.cos = a->cos; p.sin = a->sin; p.table_stride = a->table_stride;
+    p.seqlen = (int32_t)a->rows; p.heads = (int32_t)a->heads; p.n_tensors = 2;
+    p.head_dim = (int32_t)D; p.rotary_dim = (int32_t)R; p.w_f32 = a->w_dtype == H3A_DTYPE_F32;
+    p.rows = a->rows * 2 * a->heads;
+    p.div_heads = h3a::make_fast_div((uint32_t)a->heads);
+    p.div_tensors = h3a::make_fast_div(2u);
+    p.div_seqlen = h3a::make_fast_div((uint32_t)a->rows);
+    p.div_hpg = h3a::make_fast_div((uint32_t)hl);
+    if (!h3a::qknorm_rope_fast_path(p))
+        return fail(H3A_EUNSUPPORTED,
+                    "h3a_qknorm_rope_pack: rotary_dim %lld needs a multiple of 16 and 16-byte aligned cos/sin rows; "
+                    "use h3a_qknorm_rope then h3a_pack_qkv",
+                    (long long)R);
+    hipError_t e = h3a::launch_qknorm_rope(p, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_qknorm_rope_pack: launch failed: %s", hipGetErrorString(e));
     return H3A_OK;
 }
 

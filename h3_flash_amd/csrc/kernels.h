@@ -76,8 +76,44 @@ struct QkNormRopeParams {
     int32_t head_dim;
     int32_t rotary_dim;
     int32_t w_f32;  // 1: weights are fp32, 0: bf16
+    // Grouped output heads (fast path only): head h of y is stored at
+    // (h / hpg) * y_sg + (h % hpg) * y_sh; hpg == heads means ungrouped.
+    FastDiv div_hpg;
+    int64_t y_sg[2];
+    // Optional third tensor copied verbatim (no arithmetic) into the same
+    // grouped layout (fast path only; NULL: none).
+    const void* xc;
+    void* yc;
+    int64_t xc_sb, xc_ss, xc_sh;
+    int64_t yc_sb, yc_ss, yc_sh, yc_sg;
 };
 
 hipError_t launch_qknorm_rope(const QkNormRopeParams& p, hipStream_t stream);
+// Whether launch_qknorm_rope takes the fast (lane-group-per-token) path.
+bool qknorm_rope_fast_path(const QkNormRopeParams& p);
+
+// Destination-major q/k/v pack. Byte strides; row_bytes = head_dim * element size.
+struct PackQkvParams {
+    const void* src[3];
+    void* out;
+    int64_t s_row[3], s_head[3];
+    int64_t rows;
+    int32_t row_bytes;
+    uint32_t units;          // rows * heads, < 2^31
+    FastDiv div_heads, div_hl;  // heads, heads per destination
+};
+hipError_t launch_pack_qkv(const PackQkvParams& p, bool vec, hipStream_t stream);
+
+// (world, rows, inner) -> (rows, world, inner). Byte strides.
+struct MergeHeadsParams {
+    const void* x;
+    void* out;
+    int64_t s_world, s_row;
+    int64_t rows;
+    int64_t inner_bytes;
+    uint32_t vectors;            // rows * world * inner_bytes / 16 (vector path), < 2^31
+    FastDiv div_inner, div_world;  // inner_bytes / 16, world
+};
+hipError_t launch_merge_heads(const MergeHeadsParams& p, bool vec, hipStream_t stream);
 
 }  // namespace h3a

@@ -55,6 +55,12 @@ __device__ __forceinline__ void load_w8(const void* w, int col0, bool f32, float
     }
 }
 
+// Element offset of output head h: (h / hpg) * sg + (h % hpg) * sh.
+__device__ __forceinline__ int64_t head_ofs(const QkNormRopeParams& p, int h, int64_t sh, int64_t sg) {
+    const uint32_t g = fdiv((uint32_t)h, p.div_hpg);
+    return (int64_t)g * sg + (int64_t)((uint32_t)h - g * p.div_hpg.d) * sh;
+}
+
 struct RowRef {
     const uint16_t* x;
     uint16_t* y;
@@ -121,6 +127,7 @@ __global__ __launch_bounds__(kThreads) void qknorm_rope_kernel(QkNormRopeParams 
         const void* w = second ? p.w[1] : p.w[0];
         const float eps = second ? p.eps[1] : p.eps[0];
         const int64_t xsh = second ? p.x_sh[1] : p.x_sh[0], ysh = second ? p.y_sh[1] : p.y_sh[0];
+        const int64_t ysg = second ? p.y_sg[1] : p.y_sg[0];
         const uint16_t* xt = (const uint16_t*)(second ? p.x[1] : p.x[0]) + b * (second ? p.x_sb[1] : p.x_sb[0]) +
                              (int64_t)s * (second ? p.x_ss[1] : p.x_ss[0]) + col0;
         uint16_t* yt = (uint16_t*)(second ? p.y[1] : p.y[0]) + b * (second ? p.y_sb[1] : p.y_sb[0]) +
@@ -169,7 +176,24 @@ __global__ __launch_bounds__(kThreads) void qknorm_rope_kernel(QkNormRopeParams 
                 i32x4 packed;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) packed[e] = (int)pack_bf16x2(out[2 * e], out[2 * e + 1]);
-                __builtin_nontemporal_store(packed, (i32x4*)(yt + (int64_t)(h0 + i) * ysh));
+                __builtin_nontemporal_store(packed, (i32x4*)(yt + head_ofs(p, h0 + i, ysh, ysg)));
+            }
+        }
+    }
+
+    // Verbatim copy of the third tensor into the same grouped layout.
+    if (p.xc != nullptr) {
+        const uint16_t* xt = (const uint16_t*)p.xc + b * p.xc_sb + (int64_t)s * p.xc_ss + col0;
+        uint16_t* yt = (uint16_t*)p.yc + b * p.yc_sb + (int64_t)s * p.yc_ss + col0;
+        for (int h0 = 0; h0 < H; h0 += kChunk) {
+            i32x4 raw[kChunk];
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i)
+                if (h0 + i < H && on) raw[i] = __builtin_nontemporal_load((const i32x4*)(xt + (int64_t)(h0 + i) * p.xc_sh));
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i) {
+                if (h0 + i >= H) break;  // uniform
+                if (on) __builtin_nontemporal_store(raw[i], (i32x4*)(yt + head_ofs(p, h0 + i, p.yc_sh, p.yc_sg)));
             }
         }
     }
@@ -239,10 +263,15 @@ hipError_t launch_l(const QkNormRopeParams& p, bool fast, hipStream_t stream) {
 
 }  // namespace
 
+bool qknorm_rope_fast_path(const QkNormRopeParams& p) {
+    if (p.rotary_dim == 0) return true;
+    const bool aligned = ((uintptr_t)p.cos % 16 == 0) && ((uintptr_t)p.sin % 16 == 0) && (p.table_stride % 4 == 0);
+    return (p.rotary_dim % 16 == 0) && aligned;
+}
+
 hipError_t launch_qknorm_rope(const QkNormRopeParams& p, hipStream_t stream) {
     if (p.rows <= 0) return hipSuccess;
-    const bool aligned = ((uintptr_t)p.cos % 16 == 0) && ((uintptr_t)p.sin % 16 == 0) && (p.table_stride % 4 == 0);
-    const bool fast = (p.rotary_dim % 16 == 0) && aligned;
+    const bool fast = qknorm_rope_fast_path(p);
     int lanes = 1;
     while (lanes * 8 < p.head_dim) lanes <<= 1;
     switch (lanes) {

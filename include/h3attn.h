@@ -16,6 +16,16 @@
  *                     src/h3_flash/runtime/kernels/transformer.py:160-173; here
  *                     both tensors are normalised and rotated in one launch.
  *
+ * Three more replace the data movement on either side of the packed-Ulysses
+ * exchange (src/h3_flash/runtime/parallel/packed_ulysses.py:85-128):
+ *
+ *   h3a_pack_qkv          pack_qkv_destination_major / _pack_qkv_kernel
+ *                         (src/h3_flash/runtime/parallel/relayout.py:11-49,97-130)
+ *   h3a_merge_heads       merge_heads / _merge_heads_kernel (relayout.py:52-67,133-159)
+ *   h3a_qknorm_rope_pack  the per-rank sequence fused_qknorm_rope(q),
+ *                         fused_qknorm_rope(k), pack_qkv_destination_major(q, k, v)
+ *                         (packed_ulysses.py:177-200) as one launch.
+ *
  * Conventions
  *   - All tensor pointers are device pointers allocated by the caller; the
  *     library allocates nothing and keeps no per-call state (an attention
@@ -41,7 +51,7 @@ extern "C" {
 /* The library is built with hidden visibility; only these symbols export. */
 #define H3A_API __attribute__((visibility("default")))
 
-#define H3A_ABI_VERSION 2
+#define H3A_ABI_VERSION 3
 
 #define H3A_OK 0
 #define H3A_EINVAL (-1)       /* invalid argument (shape, stride, pointer) */
@@ -153,6 +163,88 @@ typedef struct h3a_qknorm_rope_args {
 } h3a_qknorm_rope_args;
 
 H3A_API int h3a_qknorm_rope(const h3a_qknorm_rope_args *args, void *stream);
+
+/*
+ * Destination-major pack of q, k, v for the packed-Ulysses QKV exchange:
+ *   out[dest][row][lh][i*head_dim + d] = X_i[row][dest*hl + lh][d]
+ * with X = (q, k, v), hl = heads / world, and out contiguous of shape
+ * (world, rows, hl, 3*head_dim). Elements of elem_bytes (1, 2, 4 or 8) bytes
+ * are moved, never converted. q/k/v are (rows, heads, head_dim) with element
+ * strides {row, head} and a contiguous last dimension. heads must be a
+ * multiple of world (H3A_EINVAL otherwise, with the reference's message).
+ */
+typedef struct h3a_pack_qkv_args {
+    int32_t abi_version;
+    const void *q;
+    const void *k;
+    const void *v;
+    void *out;
+    int64_t elem_bytes;
+    int64_t rows;
+    int64_t heads;
+    int64_t head_dim;
+    int64_t world;
+    int64_t q_stride[2]; /* row, head */
+    int64_t k_stride[2];
+    int64_t v_stride[2];
+} h3a_pack_qkv_args;
+
+H3A_API int h3a_pack_qkv(const h3a_pack_qkv_args *args, void *stream);
+
+/*
+ * Source-rank / row transpose after the output exchange:
+ *   out[row][src][t] = x[src][row][t],  t < inner (= heads_local * head_dim)
+ * x has element strides {world, row} and a contiguous inner dimension; out is
+ * contiguous (rows, world, inner). Elements are moved, never converted.
+ */
+typedef struct h3a_merge_heads_args {
+    int32_t abi_version;
+    const void *x;
+    void *out;
+    int64_t elem_bytes;
+    int64_t world;
+    int64_t rows;
+    int64_t inner;
+    int64_t x_stride[2]; /* world, row */
+} h3a_merge_heads_args;
+
+H3A_API int h3a_merge_heads(const h3a_merge_heads_args *args, void *stream);
+
+/*
+ * h3a_qknorm_rope on q and k plus h3a_pack_qkv in one launch: q and k
+ * ((rows, heads, head_dim) bf16, strides {row, head}) are normalised and
+ * rotated exactly as by h3a_qknorm_rope (same arithmetic, same rounding) and
+ * written, with v copied verbatim, into the destination-major buffer `out`
+ * of h3a_pack_qkv. Batch is 1 (the packed path's only case). Requires a
+ * rotary width that is a multiple of 16 (or 0) and 16-byte aligned cos/sin
+ * rows; other widths return H3A_EUNSUPPORTED (compose h3a_qknorm_rope and
+ * h3a_pack_qkv instead).
+ */
+typedef struct h3a_qknorm_rope_pack_args {
+    int32_t abi_version;
+    const void *q;
+    const void *k;
+    const void *v;
+    void *out;
+    const void *wq;
+    const void *wk;
+    int32_t w_dtype;
+    const float *cos;
+    const float *sin;
+    int64_t table_stride;
+    int64_t rows;
+    int64_t heads;
+    int64_t head_dim;
+    int64_t rotary_dim;
+    int64_t world;
+    int64_t q_stride[2]; /* row, head */
+    int64_t k_stride[2];
+    int64_t v_stride[2];
+    float eps_q;
+    float eps_k;
+} h3a_qknorm_rope_pack_args;
+
+H3A_API int h3a_qknorm_rope_pack(const h3a_qknorm_rope_pack_args *args, void *stream);
 
 /* Message of the last failed call on this thread ("" if none). */
 H3A_API const char *h3a_last_error(void);

@@ -37,7 +37,10 @@ def test_header_declares_the_expected_entry_points():
         "h3a_attn_fwd",
         "h3a_attn_fwd_workspace_size",
         "h3a_last_error",
+        "h3a_merge_heads",
+        "h3a_pack_qkv",
         "h3a_qknorm_rope",
+        "h3a_qknorm_rope_pack",
     ]
 
 
@@ -48,7 +51,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_abi_version(lib):
-    assert lib.h3a_abi_version() == _ext.ABI_VERSION == 2
+    assert lib.h3a_abi_version() == _ext.ABI_VERSION == 3
 
 
 def _attn_args(**overrides):
@@ -150,4 +153,117 @@ def _rope_args(**overrides):
 def test_rope_validation(lib, overrides, code, message):
     a = _rope_args(**overrides)
     assert lib.h3a_qknorm_rope(ctypes.byref(a), None) == code
+    assert message in _ext.last_error(lib)
+
+
+def _pack_args(**overrides):
+    a = _ext.PackQkvArgs()
+    a.abi_version = _ext.ABI_VERSION
+    a.q = a.k = a.v = 1 << 20
+    a.out = 1 << 22
+    a.elem_bytes = 2
+    a.rows, a.heads, a.head_dim, a.world = 4, 8, 128, 2
+    for name in ("q_stride", "k_stride", "v_stride"):
+        getattr(a, name)[:] = (8 * 128, 128)
+    for k, v in overrides.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "overrides, code, message",
+    [
+        ({"abi_version": 1}, _ext.H3A_EINVAL, "abi_version"),
+        ({"heads": 6, "world": 4}, _ext.H3A_EINVAL, "heads (6) must divide Ulysses degree (4)"),
+        ({"elem_bytes": 3}, _ext.H3A_EINVAL, "elem_bytes"),
+        ({"world": 0}, _ext.H3A_EINVAL, "extents"),
+        ({"head_dim": 0}, _ext.H3A_EINVAL, "extents"),
+        ({"v": None}, _ext.H3A_EINVAL, "NULL"),
+        ({"rows": 1 << 28}, _ext.H3A_EUNSUPPORTED, "2^31"),
+    ],
+)
+@host_only
+def test_pack_validation(lib, overrides, code, message):
+    a = _pack_args(**overrides)
+    assert lib.h3a_pack_qkv(ctypes.byref(a), None) == code
+    assert message in _ext.last_error(lib)
+
+
+@host_only
+def test_pack_negative_stride_and_empty(lib):
+    a = _pack_args()
+    a.k_stride[:] = (-1024, 128)
+    assert lib.h3a_pack_qkv(ctypes.byref(a), None) == _ext.H3A_EINVAL
+    assert lib.h3a_pack_qkv(ctypes.byref(_pack_args(rows=0)), None) == _ext.H3A_OK
+    assert lib.h3a_pack_qkv(None, None) == _ext.H3A_EINVAL
+
+
+def _merge_args(**overrides):
+    a = _ext.MergeHeadsArgs()
+    a.abi_version = _ext.ABI_VERSION
+    a.x, a.out = 1 << 20, 1 << 22
+    a.elem_bytes, a.world, a.rows, a.inner = 2, 4, 8, 640
+    a.x_stride[:] = (8 * 640, 640)
+    for k, v in overrides.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "overrides, code, message",
+    [
+        ({"abi_version": 9}, _ext.H3A_EINVAL, "abi_version"),
+        ({"elem_bytes": 0}, _ext.H3A_EINVAL, "elem_bytes"),
+        ({"world": 0}, _ext.H3A_EINVAL, "extents"),
+        ({"rows": -1}, _ext.H3A_EINVAL, "extents"),
+        ({"x": None}, _ext.H3A_EINVAL, "NULL"),
+    ],
+)
+@host_only
+def test_merge_validation(lib, overrides, code, message):
+    a = _merge_args(**overrides)
+    assert lib.h3a_merge_heads(ctypes.byref(a), None) == code
+    assert message in _ext.last_error(lib)
+
+
+@host_only
+def test_merge_empty(lib):
+    assert lib.h3a_merge_heads(ctypes.byref(_merge_args(rows=0)), None) == _ext.H3A_OK
+    assert lib.h3a_merge_heads(ctypes.byref(_merge_args(inner=0)), None) == _ext.H3A_OK
+
+
+def _rope_pack_args(**overrides):
+    a = _ext.QkNormRopePackArgs()
+    a.abi_version = _ext.ABI_VERSION
+    a.q = a.k = a.v = a.wq = a.wk = 1 << 20
+    a.out = 1 << 22
+    a.cos = a.sin = 1 << 21
+    a.table_stride = 128
+    a.rows, a.heads, a.head_dim, a.rotary_dim, a.world = 4, 8, 128, 128, 2
+    for name in ("q_stride", "k_stride", "v_stride"):
+        getattr(a, name)[:] = (8 * 128, 128)
+    a.eps_q = a.eps_k = 1e-5
+    for k, v in overrides.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "overrides, code, message",
+    [
+        ({"abi_version": 2}, _ext.H3A_EINVAL, "abi_version"),
+        ({"rotary_dim": 7}, _ext.H3A_EINVAL, "even rotary dimension no wider than the head"),
+        ({"heads": 8, "world": 3}, _ext.H3A_EINVAL, "heads (8) must divide Ulysses degree (3)"),
+        ({"rotary_dim": 42}, _ext.H3A_EUNSUPPORTED, "h3a_qknorm_rope then h3a_pack_qkv"),
+        ({"cos": (1 << 21) + 4}, _ext.H3A_EUNSUPPORTED, "aligned"),
+        ({"head_dim": 100, "rotary_dim": 96}, _ext.H3A_EUNSUPPORTED, "multiple of 8"),
+        ({"out": None}, _ext.H3A_EINVAL, "NULL"),
+        ({"k": (1 << 20) + 2}, _ext.H3A_EINVAL, "aligned"),
+        ({"w_dtype": 3}, _ext.H3A_EINVAL, "weight dtype"),
+    ],
+)
+@host_only
+def test_rope_pack_validation(lib, overrides, code, message):
+    a = _rope_pack_args(**overrides)
+    assert lib.h3a_qknorm_rope_pack(ctypes.byref(a), None) == code
     assert message in _ext.last_error(lib)
