@@ -45,6 +45,7 @@ def parse_args(argv=None):
     p.add_argument("--cpu-rows", type=int, default=0, help="query rows in the CPU baseline sample (0: all)")
     p.add_argument("--cpu-repeats", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-relayout", action="store_true", help="skip the packed-Ulysses relayout rates")
     p.add_argument(
         "--copy-calibration",
         type=int,
@@ -114,6 +115,66 @@ def cpu_baseline(torch, q, k, v, heads, rows: int, repeats: int) -> dict:
             f"(4*rows*S*D*H = {flops:.3e} flop), median of {repeats} after a 512-row warm-up "
             f"({', '.join(f'{s:.2f}' for s in samples)} s); host {cpu_model()}, {cores} cores in affinity"
         ),
+    }
+
+
+def _time_ms(torch, fn, reps: int = 20) -> float:
+    """Mean duration of ``fn`` from HIP events on the current stream."""
+
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in evs:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return statistics.fmean(a.elapsed_time(b) for a, b in evs)
+
+
+def relayout_rates(torch, world: int = 8, heads: int = 40, seqlen: int = 49920, head_dim: int = 128) -> dict:
+    """HBM rates of the packed-Ulysses relayouts on one rank's share of the
+    480p/5s geometry (all heads, seqlen / world rows): the q/k/v pack, the
+    output merge, and the fused q/k RMSNorm + RoPE + pack against the
+    unfused prologue + pack it replaces."""
+
+    from h3_flash_amd.prologue import fused_qk_norm_rope
+    from h3_flash_amd.relayout import merge_heads, pack_qkv_destination_major, qknorm_rope_pack_qkv
+    from h3_flash_amd.rope import rope_3d_tables
+
+    dev = torch.device("cuda:0")
+    rows, hl = seqlen // world, heads // world
+    g = torch.Generator(device=dev).manual_seed(11)
+    q, k, v = (torch.randn((rows, heads, head_dim), device=dev, generator=g).to(torch.bfloat16) for _ in range(3))
+    w = torch.ones(head_dim, dtype=torch.bfloat16, device=dev)
+    cos, sin = rope_3d_tables((32 // world, 30, 52))
+    cos, sin = cos.to(dev), sin.to(dev)
+    x = torch.randn((world, rows, hl, head_dim), device=dev, generator=g).to(torch.bfloat16)
+    elem = rows * heads * head_dim * 2  # one (rows, heads, head_dim) bf16 tensor
+    table = 2 * rows * cos.shape[1] * 4
+
+    def rate(name, ms, nbytes):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        return {"kernel": name, "ms": ms, "bytes_per_launch": nbytes, "GB_s": gbs, "frac_of_hbm_peak": gbs / PEAK_HBM_GBS}
+
+    pack_ms = _time_ms(torch, lambda: pack_qkv_destination_major(q, k, v, world))
+    merge_ms = _time_ms(torch, lambda: merge_heads(x))
+    fused_ms = _time_ms(torch, lambda: qknorm_rope_pack_qkv(q, k, v, w, w, cos, sin, 1e-5, 1e-5, world))
+
+    def unfused():
+        qn, kn = fused_qk_norm_rope(q.unsqueeze(0), k.unsqueeze(0), w, w, cos, sin, 1e-5, 1e-5)
+        pack_qkv_destination_major(qn.squeeze(0), kn.squeeze(0), v, world)
+
+    unfused_ms = _time_ms(torch, unfused)
+    return {
+        "workload": f"one rank of {world}-way Ulysses at S={seqlen}: {rows} rows x {heads} heads x {head_dim}, bf16",
+        "pack_qkv": rate("pack_qkv_kernel<16>", pack_ms, 2 * 3 * elem),
+        "merge_heads": rate("merge_heads_kernel", merge_ms, 2 * elem),
+        "qknorm_rope_pack": rate("qknorm_rope_kernel<16> (grouped output + v copy)", fused_ms, 2 * 3 * elem + table),
+        "unfused_prologue_then_pack_ms": unfused_ms,
+        "fused_speedup": unfused_ms / fused_ms,
     }
 
 
@@ -273,6 +334,7 @@ def main(argv=None) -> int:
         "wall_s_timed_region": wall,
         "device": torch.cuda.get_device_name(0),
     }
+    result["relayout"] = None if args.no_relayout else relayout_rates(torch)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, q, k, v, w.heads, args.cpu_rows, args.cpu_repeats)
     else:

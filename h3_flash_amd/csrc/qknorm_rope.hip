@@ -27,6 +27,7 @@ FastDiv make_fast_div(uint32_t d) {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kHeadChunk = 8;  // heads per lane group in the fast path
 
 __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) { return (__umulhi(n, f.m) + n) >> f.s; }
 
@@ -90,19 +91,24 @@ __device__ __forceinline__ RowRef locate(const QkNormRopeParams& p, uint32_t row
 // Fast path: R % 16 == 0 and 16-byte aligned tables, so a lane's 8 columns
 // are either all rotary or all pass-through, its partner columns are the 8
 // columns of lane (j +- R/16), and cos/sin come in two 16-byte loads.
-// One lane group per token: it reads the token's cos/sin once and walks the
-// token's rows tensor by tensor, kChunk heads at a time with all their loads
-// issued first; tensor and head are uniform over the block (scalar indexing).
-// Every byte of x and y is touched once: non-temporal accesses.
-template <int L>
-__global__ __launch_bounds__(kThreads) void qknorm_rope_kernel(QkNormRopeParams p) {
+// One lane group per (token, chunk of kChunk heads): it reads the token's
+// cos/sin once and walks its heads tensor by tensor, each tensor's loads
+// issued first (with a copied third tensor, all loads of the block first);
+// tensor and head are uniform over the block (scalar indexing).
+// Splitting heads over blockIdx.y keeps the grid wide for short shards with
+// many heads (a Ulysses rank's 6,240 rows x 40 heads). Every byte of x and y
+// is touched once: non-temporal accesses.
+template <int L, bool kCopy>
+__global__ __launch_bounds__(kThreads, kCopy ? 3 : 4) void qknorm_rope_kernel(QkNormRopeParams p) {
     constexpr int kGroups = kThreads / L;
-    constexpr int kChunk = 8;
+    constexpr int kChunk = kHeadChunk;
     const int tid = threadIdx.x;
     const int j = tid % L;
     const int s = (int)blockIdx.x * kGroups + tid / L;  // token
-    const int64_t b = blockIdx.y;
-    const int D = p.head_dim, R = p.rotary_dim, half = R >> 1, H = p.heads;
+    const int64_t b = blockIdx.z;
+    const int D = p.head_dim, R = p.rotary_dim, half = R >> 1;
+    const int hb = (int)blockIdx.y * kChunk;  // this block's heads: [hb, H)
+    const int H = min(p.heads, hb + kChunk);
     const int col0 = j * 8;
     const bool on = s < p.seqlen && col0 < D;
     const bool rot = col0 < R;
@@ -122,78 +128,109 @@ __global__ __launch_bounds__(kThreads) void qknorm_rope_kernel(QkNormRopeParams 
         sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w; sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
     }
 
-    for (int which = 0; which < p.n_tensors; ++which) {
-        const bool second = which != 0;
-        const void* w = second ? p.w[1] : p.w[0];
-        const float eps = second ? p.eps[1] : p.eps[0];
-        const int64_t xsh = second ? p.x_sh[1] : p.x_sh[0], ysh = second ? p.y_sh[1] : p.y_sh[0];
-        const int64_t ysg = second ? p.y_sg[1] : p.y_sg[0];
-        const uint16_t* xt = (const uint16_t*)(second ? p.x[1] : p.x[0]) + b * (second ? p.x_sb[1] : p.x_sb[0]) +
-                             (int64_t)s * (second ? p.x_ss[1] : p.x_ss[0]) + col0;
-        uint16_t* yt = (uint16_t*)(second ? p.y[1] : p.y[0]) + b * (second ? p.y_sb[1] : p.y_sb[0]) +
-                       (int64_t)s * (second ? p.y_ss[1] : p.y_ss[0]) + col0;
-        float wv[8], wp[8];
-        if (on) load_w8(w, col0, wf, wv);
-        if (on && rot) load_w8(w, src * 8, wf, wp);
-        for (int h0 = 0; h0 < H; h0 += kChunk) {
+    // Normalise, rotate and store one row chunk (all L lanes of the group join
+    // the reductions and the partner shuffle).
+    auto row = [&](const i32x4& x, const float* wv, const float* wp, float eps, uint16_t* dst) __attribute__((always_inline)) {
+        float xv[8];
+        unpack8(x, xv);
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += xv[e] * xv[e];
+#pragma unroll
+        for (int off = L / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, L);
+        const float r = rsqrtf((d_pow2 ? ss * inv_d : ss / (float)D) + eps);
+        // Partner chunk lives in lane src of the same row.
+        i32x4 praw;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) praw[e] = __shfl(x[e], src, L);
+        if (!on) return;
+        float out[8];
+        if (rot) {
+            float xp[8];
+            unpack8(praw, xp);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float n = xv[e] * r * wv[e];
+                const float pn = xp[e] * r * wp[e];
+                const float rt = first ? -pn : pn;
+                out[e] = n * cv[e] + rt * sv[e];
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) out[e] = xv[e] * r * wv[e];
+        }
+        i32x4 packed;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) packed[e] = (int)pack_bf16x2(out[2 * e], out[2 * e + 1]);
+        __builtin_nontemporal_store(packed, (i32x4*)dst);
+    };
+    const int nh = H - hb;  // heads of this block (uniform)
+    auto x_at = [&](int which, int i) {
+        return (const i32x4*)((const uint16_t*)p.x[which] + b * p.x_sb[which] + (int64_t)s * p.x_ss[which] + col0 +
+                              (int64_t)(hb + i) * p.x_sh[which]);
+    };
+    auto y_at = [&](int which, int i) {
+        return (uint16_t*)p.y[which] + b * p.y_sb[which] + (int64_t)s * p.y_ss[which] + col0 +
+               head_ofs(p, hb + i, p.y_sh[which], p.y_sg[which]);
+    };
+
+    if constexpr (kCopy) {
+        // Pack mode: every load of the block (q, k and the copied tensor) is
+        // issued before any arithmetic; the shard is short, so this is where
+        // the memory parallelism comes from.
+        i32x4 raw[2][kChunk], rawc[kChunk];
+        const uint16_t* xc = (const uint16_t*)p.xc + b * p.xc_sb + (int64_t)s * p.xc_ss + col0;
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) {
+#pragma unroll
+            for (int which = 0; which < 2; ++which) {
+                raw[which][i] = i32x4{0, 0, 0, 0};
+                if (i < nh && on) raw[which][i] = __builtin_nontemporal_load(x_at(which, i));
+            }
+            if (i < nh && on) rawc[i] = __builtin_nontemporal_load((const i32x4*)(xc + (int64_t)(hb + i) * p.xc_sh));
+        }
+#pragma unroll
+        for (int which = 0; which < 2; ++which) {
+            float wv[8], wp[8];
+            if (on) load_w8(p.w[which], col0, wf, wv);
+            if (on && rot) load_w8(p.w[which], src * 8, wf, wp);
+#pragma unroll
+            for (int i = 0; i < kChunk; ++i) {
+                if (i >= nh) break;  // uniform
+                row(raw[which][i], wv, wp, p.eps[which], y_at(which, i));
+            }
+        }
+        uint16_t* yc = (uint16_t*)p.yc + b * p.yc_sb + (int64_t)s * p.yc_ss + col0;
+#pragma unroll
+        for (int i = 0; i < kChunk; ++i) {
+            if (i >= nh) break;  // uniform
+            if (on) __builtin_nontemporal_store(rawc[i], (i32x4*)(yc + head_ofs(p, hb + i, p.yc_sh, p.yc_sg)));
+        }
+    } else {
+        // Tensor by tensor, each tensor's loads issued first.
+        for (int which = 0; which < p.n_tensors; ++which) {
+            const bool second = which != 0;
+            const void* w = second ? p.w[1] : p.w[0];
+            const float eps = second ? p.eps[1] : p.eps[0];
+            const int64_t xsh = second ? p.x_sh[1] : p.x_sh[0], ysh = second ? p.y_sh[1] : p.y_sh[0];
+            const int64_t ysg = second ? p.y_sg[1] : p.y_sg[0];
+            const uint16_t* xt = (const uint16_t*)(second ? p.x[1] : p.x[0]) + b * (second ? p.x_sb[1] : p.x_sb[0]) +
+                                 (int64_t)s * (second ? p.x_ss[1] : p.x_ss[0]) + col0;
+            uint16_t* yt = (uint16_t*)(second ? p.y[1] : p.y[0]) + b * (second ? p.y_sb[1] : p.y_sb[0]) +
+                           (int64_t)s * (second ? p.y_ss[1] : p.y_ss[0]) + col0;
+            float wv[8], wp[8];
+            if (on) load_w8(w, col0, wf, wv);
+            if (on && rot) load_w8(w, src * 8, wf, wp);
             i32x4 raw[kChunk];
 #pragma unroll
             for (int i = 0; i < kChunk; ++i) {
                 raw[i] = i32x4{0, 0, 0, 0};
-                if (h0 + i < H && on) raw[i] = __builtin_nontemporal_load((const i32x4*)(xt + (int64_t)(h0 + i) * xsh));
+                if (i < nh && on) raw[i] = __builtin_nontemporal_load((const i32x4*)(xt + (int64_t)(hb + i) * xsh));
             }
 #pragma unroll
             for (int i = 0; i < kChunk; ++i) {
-                if (h0 + i >= H) break;  // uniform
-                float xv[8];
-                unpack8(raw[i], xv);
-                float ss = 0.f;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) ss += xv[e] * xv[e];
-#pragma unroll
-                for (int off = L / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, L);
-                const float r = rsqrtf((d_pow2 ? ss * inv_d : ss / (float)D) + eps);
-                // Partner chunk lives in lane src of the same row (all lanes join).
-                i32x4 praw;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) praw[e] = __shfl(raw[i][e], src, L);
-                if (!on) continue;
-                float out[8];
-                if (rot) {
-                    float xp[8];
-                    unpack8(praw, xp);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) {
-                        const float n = xv[e] * r * wv[e];
-                        const float pn = xp[e] * r * wp[e];
-                        const float rt = first ? -pn : pn;
-                        out[e] = n * cv[e] + rt * sv[e];
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) out[e] = xv[e] * r * wv[e];
-                }
-                i32x4 packed;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) packed[e] = (int)pack_bf16x2(out[2 * e], out[2 * e + 1]);
-                __builtin_nontemporal_store(packed, (i32x4*)(yt + head_ofs(p, h0 + i, ysh, ysg)));
-            }
-        }
-    }
-
-    // Verbatim copy of the third tensor into the same grouped layout.
-    if (p.xc != nullptr) {
-        const uint16_t* xt = (const uint16_t*)p.xc + b * p.xc_sb + (int64_t)s * p.xc_ss + col0;
-        uint16_t* yt = (uint16_t*)p.yc + b * p.yc_sb + (int64_t)s * p.yc_ss + col0;
-        for (int h0 = 0; h0 < H; h0 += kChunk) {
-            i32x4 raw[kChunk];
-#pragma unroll
-            for (int i = 0; i < kChunk; ++i)
-                if (h0 + i < H && on) raw[i] = __builtin_nontemporal_load((const i32x4*)(xt + (int64_t)(h0 + i) * p.xc_sh));
-#pragma unroll
-            for (int i = 0; i < kChunk; ++i) {
-                if (h0 + i >= H) break;  // uniform
-                if (on) __builtin_nontemporal_store(raw[i], (i32x4*)(yt + head_ofs(p, h0 + i, p.yc_sh, p.yc_sg)));
+                if (i >= nh) break;  // uniform
+                row(raw[i], wv, wp, eps, yt + head_ofs(p, hb + i, ysh, ysg));
             }
         }
     }
@@ -251,8 +288,12 @@ template <int L>
 hipError_t launch_l(const QkNormRopeParams& p, bool fast, hipStream_t stream) {
     if (fast) {
         const int64_t batch = p.rows / ((int64_t)p.seqlen * p.n_tensors * p.heads);
-        const dim3 grid((unsigned)((p.seqlen + kThreads / L - 1) / (kThreads / L)), (unsigned)batch);
-        hipLaunchKernelGGL((qknorm_rope_kernel<L>), grid, dim3(kThreads), 0, stream, p);
+        const dim3 grid((unsigned)((p.seqlen + kThreads / L - 1) / (kThreads / L)), (unsigned)((p.heads + kHeadChunk - 1) / kHeadChunk),
+                        (unsigned)batch);
+        if (p.xc != nullptr)
+            hipLaunchKernelGGL((qknorm_rope_kernel<L, true>), grid, dim3(kThreads), 0, stream, p);
+        else
+            hipLaunchKernelGGL((qknorm_rope_kernel<L, false>), grid, dim3(kThreads), 0, stream, p);
     } else {
         const int64_t per_block = kThreads / L;
         const unsigned blocks = (unsigned)((p.rows + per_block - 1) / per_block);
