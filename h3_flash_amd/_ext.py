@@ -23,6 +23,8 @@ H3A_ELAUNCH = -3
 
 H3A_DTYPE_BF16 = 0
 H3A_DTYPE_F32 = 1
+H3A_DTYPE_I32 = 2
+H3A_DTYPE_I64 = 3
 
 _I64x3 = ctypes.c_int64 * 3
 _I64x2 = ctypes.c_int64 * 2
@@ -141,6 +143,72 @@ class QkNormRopePackArgs(ctypes.Structure):
     ]
 
 
+class RmsnormModulateArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("x", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("weight", ctypes.c_void_p),
+        ("w_dtype", ctypes.c_int32),
+        ("scale", ctypes.c_void_p),
+        ("shift", ctypes.c_void_p),
+        ("table_dtype", ctypes.c_int32),
+        ("scale_stride", ctypes.c_int64),
+        ("shift_stride", ctypes.c_int64),
+        ("table_rows", ctypes.c_int64),
+        ("index", ctypes.c_void_p),
+        ("index_dtype", ctypes.c_int32),
+        ("n_index", ctypes.c_int64),
+        ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64),
+        ("x_stride", ctypes.c_int64),
+        ("out_stride", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class ResidualGateRmsnormModulateArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("residual", ctypes.c_void_p),
+        ("branch", ctypes.c_void_p),
+        ("hidden_out", ctypes.c_void_p),
+        ("normed_out", ctypes.c_void_p),
+        ("weight", ctypes.c_void_p),
+        ("w_dtype", ctypes.c_int32),
+        ("gate", ctypes.c_void_p),
+        ("scale", ctypes.c_void_p),
+        ("shift", ctypes.c_void_p),
+        ("table_dtype", ctypes.c_int32),
+        ("gate_stride", ctypes.c_int64),
+        ("scale_stride", ctypes.c_int64),
+        ("shift_stride", ctypes.c_int64),
+        ("table_rows", ctypes.c_int64),
+        ("index", ctypes.c_void_p),
+        ("index_dtype", ctypes.c_int32),
+        ("n_index", ctypes.c_int64),
+        ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64),
+        ("residual_stride", ctypes.c_int64),
+        ("branch_stride", ctypes.c_int64),
+        ("hidden_stride", ctypes.c_int64),
+        ("normed_stride", ctypes.c_int64),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class SwigluArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("x", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("rows", ctypes.c_int64),
+        ("cols", ctypes.c_int64),
+        ("x_stride", ctypes.c_int64),
+        ("out_stride", ctypes.c_int64),
+    ]
+
+
 # Every function the header declares, with its ctypes signature.
 SIGNATURES = {
     "h3a_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
@@ -149,6 +217,12 @@ SIGNATURES = {
     "h3a_pack_qkv": (ctypes.c_int, [ctypes.POINTER(PackQkvArgs), ctypes.c_void_p]),
     "h3a_merge_heads": (ctypes.c_int, [ctypes.POINTER(MergeHeadsArgs), ctypes.c_void_p]),
     "h3a_qknorm_rope_pack": (ctypes.c_int, [ctypes.POINTER(QkNormRopePackArgs), ctypes.c_void_p]),
+    "h3a_rmsnorm_modulate": (ctypes.c_int, [ctypes.POINTER(RmsnormModulateArgs), ctypes.c_void_p]),
+    "h3a_residual_gate_rmsnorm_modulate": (
+        ctypes.c_int,
+        [ctypes.POINTER(ResidualGateRmsnormModulateArgs), ctypes.c_void_p],
+    ),
+    "h3a_swiglu": (ctypes.c_int, [ctypes.POINTER(SwigluArgs), ctypes.c_void_p]),
     "h3a_last_error": (ctypes.c_char_p, []),
     "h3a_abi_version": (ctypes.c_int, []),
 }

@@ -135,6 +135,52 @@ h3a::SplitPlan attn_plan(const h3a_attn_args* a, const h3a::AttnParams& p) {
     return h3a::plan_attn_split(tiles, (a->seqlen_k + bn - 1) / bn, device_cus());
 }
 
+// Shared checks of the modulation entry points. Fills the table, index and
+// weight fields of p and reports whether the 16-byte vector path applies to
+// them (activations are checked by the caller).
+int prepare_modulate(const char* fn, const void* weight, int32_t w_dtype, const void* const* tables,
+                     const int64_t* table_strides, int n_tables, int32_t table_dtype, int64_t table_rows,
+                     const void* index, int32_t index_dtype, int64_t n_index, int64_t rows, int64_t cols, float eps,
+                     h3a::ModulateParams& p, bool* vec) {
+    if (rows < 0 || cols <= 0 || cols >= ((int64_t)1 << 31) || rows >= ((int64_t)1 << 31))
+        return fail(H3A_EINVAL, "%s: bad extents (rows=%lld cols=%lld)", fn, (long long)rows, (long long)cols);
+    if (w_dtype != H3A_DTYPE_BF16 && w_dtype != H3A_DTYPE_F32) return fail(H3A_EINVAL, "%s: unknown weight dtype %d", fn, w_dtype);
+    if (table_dtype != H3A_DTYPE_BF16 && table_dtype != H3A_DTYPE_F32)
+        return fail(H3A_EINVAL, "%s: unknown table dtype %d", fn, table_dtype);
+    if (index_dtype != H3A_DTYPE_I32 && index_dtype != H3A_DTYPE_I64)
+        return fail(H3A_EINVAL, "%s: index dtype must be int32 or int64, got code %d", fn, index_dtype);
+    if (n_index <= 0 || table_rows <= 0) return fail(H3A_EINVAL, "%s: n_index and table_rows must be > 0", fn);
+    if (!(eps >= 0.f)) return fail(H3A_EINVAL, "%s: eps must be >= 0", fn);
+    if (rows > 0 && (!weight || !index)) return fail(H3A_EINVAL, "%s: NULL weight or index", fn);
+    const int64_t tsize = table_dtype == H3A_DTYPE_F32 ? 4 : 2;
+    bool v = cols % 8 == 0 && cols <= h3a::modulate_max_vector_cols() && aligned16(weight);
+    for (int i = 0; i < n_tables; ++i) {
+        if (rows > 0 && !tables[i]) return fail(H3A_EINVAL, "%s: NULL modulation table", fn);
+        if (table_strides[i] < cols) return fail(H3A_EINVAL, "%s: table row stride %lld < cols", fn, (long long)table_strides[i]);
+        v = v && aligned16(tables[i]) && (table_strides[i] * tsize) % 16 == 0;
+    }
+    p.weight = weight;
+    p.w_f32 = w_dtype == H3A_DTYPE_F32;
+    p.table_f32 = table_dtype == H3A_DTYPE_F32;
+    p.index = index;
+    p.index_i64 = index_dtype == H3A_DTYPE_I64;
+    p.n_index = n_index;
+    p.table_rows = table_rows;
+    p.rows = rows;
+    p.cols = (int32_t)cols;
+    p.eps = eps;
+    *vec = v;
+    return H3A_OK;
+}
+
+// A bf16 activation matrix: row stride >= cols; vector path needs 16-byte rows.
+int check_rows(const char* fn, const char* name, const void* ptr, int64_t stride, int64_t rows, int64_t cols, bool* vec) {
+    if (rows > 0 && !ptr) return fail(H3A_EINVAL, "%s: NULL %s", fn, name);
+    if (stride < cols) return fail(H3A_EINVAL, "%s: %s row stride %lld < cols %lld", fn, name, (long long)stride, (long long)cols);
+    *vec = *vec && aligned16(ptr) && stride % 8 == 0;
+    return H3A_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -377,6 +423,77 @@ int h3a_qknorm_rope_pack(const h3a_qknorm_rope_pack_args* a, void* stream) {
                     (long long)R);
     hipError_t e = h3a::launch_qknorm_rope(p, (hipStream_t)stream);
     if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_qknorm_rope_pack: launch failed: %s", hipGetErrorString(e));
+    return H3A_OK;
+}
+
+int h3a_rmsnorm_modulate(const h3a_rmsnorm_modulate_args* a, void* stream) {
+    g_err[0] = '\0';
+    const char* fn = "h3a_rmsnorm_modulate";
+    if (a == nullptr) return fail(H3A_EINVAL, "%s: args is NULL", fn);
+    if (a->abi_version != H3A_ABI_VERSION)
+        return fail(H3A_EINVAL, "%s: abi_version %d, library is %d", fn, a->abi_version, H3A_ABI_VERSION);
+    h3a::ModulateParams p{};
+    bool vec = false;
+    const void* tables[2] = {a->scale, a->shift};
+    const int64_t strides[2] = {a->scale_stride, a->shift_stride};
+    int rc = prepare_modulate(fn, a->weight, a->w_dtype, tables, strides, 2, a->table_dtype, a->table_rows, a->index,
+                              a->index_dtype, a->n_index, a->rows, a->cols, a->eps, p, &vec);
+    if (rc != H3A_OK) return rc;
+    if ((rc = check_rows(fn, "x", a->x, a->x_stride, a->rows, a->cols, &vec)) != H3A_OK) return rc;
+    if ((rc = check_rows(fn, "out", a->out, a->out_stride, a->rows, a->cols, &vec)) != H3A_OK) return rc;
+    if (a->rows == 0) return H3A_OK;
+    p.x = a->x; p.out = a->out; p.scale = a->scale; p.shift = a->shift;
+    p.x_stride = a->x_stride; p.out_stride = a->out_stride;
+    p.scale_stride = a->scale_stride; p.shift_stride = a->shift_stride;
+    hipError_t e = h3a::launch_modulate(p, vec, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(H3A_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+    return H3A_OK;
+}
+
+int h3a_residual_gate_rmsnorm_modulate(const h3a_residual_gate_rmsnorm_modulate_args* a, void* stream) {
+    g_err[0] = '\0';
+    const char* fn = "h3a_residual_gate_rmsnorm_modulate";
+    if (a == nullptr) return fail(H3A_EINVAL, "%s: args is NULL", fn);
+    if (a->abi_version != H3A_ABI_VERSION)
+        return fail(H3A_EINVAL, "%s: abi_version %d, library is %d", fn, a->abi_version, H3A_ABI_VERSION);
+    h3a::ModulateParams p{};
+    bool vec = false;
+    const void* tables[3] = {a->gate, a->scale, a->shift};
+    const int64_t strides[3] = {a->gate_stride, a->scale_stride, a->shift_stride};
+    int rc = prepare_modulate(fn, a->weight, a->w_dtype, tables, strides, 3, a->table_dtype, a->table_rows, a->index,
+                              a->index_dtype, a->n_index, a->rows, a->cols, a->eps, p, &vec);
+    if (rc != H3A_OK) return rc;
+    if ((rc = check_rows(fn, "residual", a->residual, a->residual_stride, a->rows, a->cols, &vec)) != H3A_OK) return rc;
+    if ((rc = check_rows(fn, "branch", a->branch, a->branch_stride, a->rows, a->cols, &vec)) != H3A_OK) return rc;
+    if ((rc = check_rows(fn, "hidden_out", a->hidden_out, a->hidden_stride, a->rows, a->cols, &vec)) != H3A_OK) return rc;
+    if ((rc = check_rows(fn, "normed_out", a->normed_out, a->normed_stride, a->rows, a->cols, &vec)) != H3A_OK) return rc;
+    if (a->rows == 0) return H3A_OK;
+    p.x = a->branch; p.residual = a->residual; p.out = a->normed_out; p.hidden = a->hidden_out;
+    p.gate = a->gate; p.scale = a->scale; p.shift = a->shift;
+    p.x_stride = a->branch_stride; p.residual_stride = a->residual_stride;
+    p.out_stride = a->normed_stride; p.hidden_stride = a->hidden_stride;
+    p.gate_stride = a->gate_stride; p.scale_stride = a->scale_stride; p.shift_stride = a->shift_stride;
+    hipError_t e = h3a::launch_modulate(p, vec, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(H3A_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+    return H3A_OK;
+}
+
+int h3a_swiglu(const h3a_swiglu_args* a, void* stream) {
+    g_err[0] = '\0';
+    const char* fn = "h3a_swiglu";
+    if (a == nullptr) return fail(H3A_EINVAL, "%s: args is NULL", fn);
+    if (a->abi_version != H3A_ABI_VERSION)
+        return fail(H3A_EINVAL, "%s: abi_version %d, library is %d", fn, a->abi_version, H3A_ABI_VERSION);
+    if (a->rows < 0 || a->cols < 0) return fail(H3A_EINVAL, "%s: bad extents", fn);
+    if (a->x_stride < 2 * a->cols || a->out_stride < a->cols)
+        return fail(H3A_EINVAL, "%s: row strides must cover the row (x: 2*cols, out: cols)", fn);
+    if (a->rows == 0 || a->cols == 0) return H3A_OK;
+    if (!a->x || !a->out) return fail(H3A_EINVAL, "%s: NULL tensor pointer", fn);
+    h3a::SwigluParams p{a->x, a->out, a->x_stride, a->out_stride, a->rows, a->cols};
+    const bool vec = a->cols % 8 == 0 && aligned16(a->x) && aligned16(a->out) && a->x_stride % 8 == 0 &&
+                     a->out_stride % 8 == 0;
+    hipError_t e = h3a::launch_swiglu(p, vec, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(H3A_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
     return H3A_OK;
 }
 

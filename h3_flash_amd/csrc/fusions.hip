@@ -1,0 +1,234 @@
+// Row-wise fusions of the MiniMax H3 DiT block around attention (gfx950).
+//
+// Arithmetic follows the reference Triton kernels
+// (src/h3_flash/runtime/kernels/fusions.py), in fp32 with one rounding on
+// store:
+//   rmsnorm_modulate (:69-96)
+//       n   = x * rsqrt(sum(x^2) / C + eps)
+//       out = n * w * (1 + scale[t]) + shift[t]
+//   residual_gate_rmsnorm_modulate (:23-67)
+//       h      = residual + gate[t] * branch          -> hidden_out
+//       n      = h * rsqrt(sum(h^2) / C + eps) * w    (h in fp32, unrounded)
+//       normed = n * (1 + scale[t]) + shift[t]        -> normed_out
+//   swiglu (:98-123)
+//       out = value * (gate * sigmoid(gate)),  value = x[:, :C], gate = x[:, C:]
+// with t = index[row % n_index] the modulation-table row of a token.
+//
+// Layout and roofline: each row kernel keeps its row in VGPRs (one 256-thread
+// workgroup per row, 16 bytes per lane per vector), so x (and residual,
+// branch) are read from HBM once and the outputs written once; weight and the
+// small modulation tables are re-read by every row and served from L2. All
+// kernels are HBM-bound. Indices outside the table are clamped to it (the
+// reference reads out of bounds there).
+#include "common.h"
+#include "kernels.h"
+
+namespace h3a {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+__device__ __forceinline__ void unpack8(i32x4 raw, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t w = (uint32_t)raw[i];
+        f[2 * i] = __uint_as_float(w << 16);
+        f[2 * i + 1] = __uint_as_float(w & 0xffff0000u);
+    }
+}
+
+__device__ __forceinline__ i32x4 pack8(const float* f) {
+    i32x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = (int)pack_bf16x2(f[2 * i], f[2 * i + 1]);
+    return r;
+}
+
+// Eight consecutive values of a bf16 or fp32 vector (16/32-byte aligned).
+__device__ __forceinline__ void load8(const void* base, int64_t idx, bool f32, float* out) {
+    if (f32) {
+        const f32x4 a = *(const f32x4*)((const float*)base + idx);
+        const f32x4 b = *(const f32x4*)((const float*)base + idx + 4);
+        out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+        out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+    } else {
+        unpack8(*(const i32x4*)((const uint16_t*)base + idx), out);
+    }
+}
+
+__device__ __forceinline__ float load1(const void* base, int64_t idx, bool f32) {
+    return f32 ? ((const float*)base)[idx] : bf16_to_f32(((const uint16_t*)base)[idx]);
+}
+
+__device__ __forceinline__ int64_t table_row(const ModulateParams& p, int64_t row) {
+    const int64_t i = row % p.n_index;
+    int64_t t = p.index_i64 ? ((const int64_t*)p.index)[i] : (int64_t)((const int32_t*)p.index)[i];
+    t = t < 0 ? 0 : t;
+    return t >= p.table_rows ? p.table_rows - 1 : t;
+}
+
+// Sum of v over the workgroup (fixed order: lanes, then waves in order).
+__device__ __forceinline__ float block_sum(float v, float* lds) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) lds[wave] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) s += lds[w];
+    return s;
+}
+
+// Vector path: C % 8 == 0, every row and table row 16-byte aligned.
+// NV = vectors of 8 per thread, NV * 8 * kThreads >= C.
+template <int NV, bool kResidual>
+__global__ __launch_bounds__(kThreads) void modulate_kernel(ModulateParams p) {
+    __shared__ float red[kWaves];
+    const int64_t row = blockIdx.x;
+    const int C = p.cols;
+    const int64_t t = table_row(p, row);
+    float h[NV][8];
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int c = (threadIdx.x + k * kThreads) * 8;
+        if (c >= C) break;
+        if constexpr (kResidual) {
+            float r[8], br[8], g[8];
+            unpack8(__builtin_nontemporal_load((const i32x4*)((const uint16_t*)p.residual + row * p.residual_stride + c)), r);
+            unpack8(__builtin_nontemporal_load((const i32x4*)((const uint16_t*)p.x + row * p.x_stride + c)), br);
+            load8(p.gate, t * p.gate_stride + c, p.table_f32, g);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[k][e] = r[e] + g[e] * br[e];
+            __builtin_nontemporal_store(pack8(h[k]), (i32x4*)((uint16_t*)p.hidden + row * p.hidden_stride + c));
+        } else {
+            unpack8(__builtin_nontemporal_load((const i32x4*)((const uint16_t*)p.x + row * p.x_stride + c)), h[k]);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += h[k][e] * h[k][e];
+    }
+    const float r = rsqrtf(block_sum(ss, red) / (float)C + p.eps);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+        const int c = (threadIdx.x + k * kThreads) * 8;
+        if (c >= C) break;
+        float w[8], sc[8], sh[8], o[8];
+        load8(p.weight, c, p.w_f32, w);
+        load8(p.scale, t * p.scale_stride + c, p.table_f32, sc);
+        load8(p.shift, t * p.shift_stride + c, p.table_f32, sh);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = h[k][e] * r * w[e] * (1.0f + sc[e]) + sh[e];
+        __builtin_nontemporal_store(pack8(o), (i32x4*)((uint16_t*)p.out + row * p.out_stride + c));
+    }
+}
+
+// Element path (any C, any alignment): two passes over the row, the second
+// re-reading x (or the unrounded residual + gate * branch) from cache.
+template <bool kResidual>
+__global__ __launch_bounds__(kThreads) void modulate_elem_kernel(ModulateParams p) {
+    __shared__ float red[kWaves];
+    const int64_t row = blockIdx.x;
+    const int C = p.cols;
+    const int64_t t = table_row(p, row);
+    auto value = [&](int c) {
+        if constexpr (kResidual) {
+            const float r = bf16_to_f32(((const uint16_t*)p.residual)[row * p.residual_stride + c]);
+            const float b = bf16_to_f32(((const uint16_t*)p.x)[row * p.x_stride + c]);
+            return r + load1(p.gate, t * p.gate_stride + c, p.table_f32) * b;
+        } else {
+            return bf16_to_f32(((const uint16_t*)p.x)[row * p.x_stride + c]);
+        }
+    };
+    float ss = 0.f;
+    for (int c = threadIdx.x; c < C; c += kThreads) {
+        const float h = value(c);
+        ss += h * h;
+        if constexpr (kResidual) {
+            const uint32_t bits = pack_bf16x2(h, 0.f);
+            ((uint16_t*)p.hidden)[row * p.hidden_stride + c] = (uint16_t)(bits & 0xffffu);
+        }
+    }
+    const float r = rsqrtf(block_sum(ss, red) / (float)C + p.eps);
+    for (int c = threadIdx.x; c < C; c += kThreads) {
+        const float o = value(c) * r * load1(p.weight, c, p.w_f32) * (1.0f + load1(p.scale, t * p.scale_stride + c, p.table_f32)) +
+                        load1(p.shift, t * p.shift_stride + c, p.table_f32);
+        const uint32_t bits = pack_bf16x2(o, 0.f);
+        ((uint16_t*)p.out)[row * p.out_stride + c] = (uint16_t)(bits & 0xffffu);
+    }
+}
+
+__device__ __forceinline__ float silu_mul(float v, float g) { return v * (g * (1.0f / (1.0f + __expf(-g)))); }
+
+// out[r, c] = x[r, c] * silu(x[r, C + c]); vector o covers 8 columns.
+__global__ __launch_bounds__(kThreads) void swiglu_kernel(SwigluParams p) {
+    const int64_t per_row = p.cols / 8;
+    const int64_t total = p.rows * per_row;
+    for (int64_t o = blockIdx.x * (int64_t)kThreads + threadIdx.x; o < total; o += (int64_t)gridDim.x * kThreads) {
+        const int64_t row = o / per_row;
+        const int64_t c = (o - row * per_row) * 8;
+        const uint16_t* x = (const uint16_t*)p.x + row * p.x_stride + c;
+        float v[8], g[8], out[8];
+        unpack8(__builtin_nontemporal_load((const i32x4*)x), v);
+        unpack8(__builtin_nontemporal_load((const i32x4*)(x + p.cols)), g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) out[e] = silu_mul(v[e], g[e]);
+        __builtin_nontemporal_store(pack8(out), (i32x4*)((uint16_t*)p.out + row * p.out_stride + c));
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void swiglu_elem_kernel(SwigluParams p) {
+    const int64_t total = p.rows * p.cols;
+    for (int64_t o = blockIdx.x * (int64_t)kThreads + threadIdx.x; o < total; o += (int64_t)gridDim.x * kThreads) {
+        const int64_t row = o / p.cols;
+        const int64_t c = o - row * p.cols;
+        const uint16_t* x = (const uint16_t*)p.x + row * p.x_stride;
+        const uint32_t bits = pack_bf16x2(silu_mul(bf16_to_f32(x[c]), bf16_to_f32(x[p.cols + c])), 0.f);
+        ((uint16_t*)p.out)[row * p.out_stride + c] = (uint16_t)(bits & 0xffffu);
+    }
+}
+
+unsigned stride_grid(int64_t work) {
+    const int64_t blocks = (work + kThreads - 1) / kThreads;
+    return (unsigned)(blocks < 65536 ? (blocks > 0 ? blocks : 1) : 65536);
+}
+
+template <bool kResidual>
+hipError_t launch_modulate_t(const ModulateParams& p, bool vec, hipStream_t stream) {
+    const dim3 grid((unsigned)p.rows), block(kThreads);
+    if (!vec) {
+        hipLaunchKernelGGL((modulate_elem_kernel<kResidual>), grid, block, 0, stream, p);
+        return hipGetLastError();
+    }
+    const int nv = (int)((p.cols + 8 * kThreads - 1) / (8 * kThreads));
+    switch (nv) {
+#define H3A_NV(n) \
+    case n: hipLaunchKernelGGL((modulate_kernel<n, kResidual>), grid, block, 0, stream, p); break;
+        H3A_NV(1) H3A_NV(2) H3A_NV(3) H3A_NV(4) H3A_NV(5) H3A_NV(6) H3A_NV(7) H3A_NV(8)
+#undef H3A_NV
+        default:
+            hipLaunchKernelGGL((modulate_elem_kernel<kResidual>), grid, block, 0, stream, p);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+int modulate_max_vector_cols() { return 8 * 8 * kThreads; }
+
+hipError_t launch_modulate(const ModulateParams& p, bool vec, hipStream_t stream) {
+    if (p.rows == 0 || p.cols == 0) return hipSuccess;
+    return p.residual != nullptr ? launch_modulate_t<true>(p, vec, stream) : launch_modulate_t<false>(p, vec, stream);
+}
+
+hipError_t launch_swiglu(const SwigluParams& p, bool vec, hipStream_t stream) {
+    if (p.rows == 0 || p.cols == 0) return hipSuccess;
+    if (vec)
+        hipLaunchKernelGGL(swiglu_kernel, dim3(stride_grid(p.rows * (p.cols / 8))), dim3(kThreads), 0, stream, p);
+    else
+        hipLaunchKernelGGL(swiglu_elem_kernel, dim3(stride_grid(p.rows * p.cols)), dim3(kThreads), 0, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace h3a

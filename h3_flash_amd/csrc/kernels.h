@@ -116,4 +116,34 @@ struct MergeHeadsParams {
 };
 hipError_t launch_merge_heads(const MergeHeadsParams& p, bool vec, hipStream_t stream);
 
+// RMSNorm + modulation rows; residual != NULL selects the residual + gate
+// variant (x is then the branch). Strides in elements.
+struct ModulateParams {
+    const void* x;
+    const void* residual;
+    void* out;
+    void* hidden;
+    const void* weight;
+    const void* gate;
+    const void* scale;
+    const void* shift;
+    const void* index;
+    int64_t x_stride, residual_stride, out_stride, hidden_stride;
+    int64_t gate_stride, scale_stride, shift_stride;
+    int64_t rows, n_index, table_rows;
+    int32_t cols;
+    int32_t w_f32, table_f32, index_i64;
+    float eps;
+};
+// Widest row the register-resident vector path takes.
+int modulate_max_vector_cols();
+hipError_t launch_modulate(const ModulateParams& p, bool vec, hipStream_t stream);
+
+struct SwigluParams {
+    const void* x;
+    void* out;
+    int64_t x_stride, out_stride, rows, cols;
+};
+hipError_t launch_swiglu(const SwigluParams& p, bool vec, hipStream_t stream);
+
 }  // namespace h3a

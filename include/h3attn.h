@@ -26,6 +26,14 @@
  *                         fused_qknorm_rope(k), pack_qkv_destination_major(q, k, v)
  *                         (packed_ulysses.py:177-200) as one launch.
  *
+ * And three replace the other Triton fusions of the DiT block
+ * (src/h3_flash/runtime/kernels/fusions.py):
+ *
+ *   h3a_rmsnorm_modulate                fused_rmsnorm_modulate (:194-215, kernel :69-96)
+ *   h3a_residual_gate_rmsnorm_modulate  fused_residual_gate_rmsnorm_modulate
+ *                                       (:218-248, kernel :23-67)
+ *   h3a_swiglu                          fused_swiglu (:251-265, kernel :98-123)
+ *
  * Conventions
  *   - All tensor pointers are device pointers allocated by the caller; the
  *     library allocates nothing and keeps no per-call state (an attention
@@ -58,9 +66,11 @@ extern "C" {
 #define H3A_EUNSUPPORTED (-2) /* valid request this build does not implement */
 #define H3A_ELAUNCH (-3)      /* the HIP launch itself failed */
 
-/* dtype codes used by h3a_qknorm_rope for the norm weights */
+/* dtype codes: norm weights and modulation tables (bf16 / fp32), table indices (int32 / int64) */
 #define H3A_DTYPE_BF16 0
 #define H3A_DTYPE_F32 1
+#define H3A_DTYPE_I32 2
+#define H3A_DTYPE_I64 3
 
 /*
  * Dense (or block-diagonal varlen) non-causal attention forward,
@@ -245,6 +255,95 @@ typedef struct h3a_qknorm_rope_pack_args {
 } h3a_qknorm_rope_pack_args;
 
 H3A_API int h3a_qknorm_rope_pack(const h3a_qknorm_rope_pack_args *args, void *stream);
+
+/*
+ * Per row r (token) with modulation-table row t = index[r % n_index]:
+ *   n      = x[r] * rsqrt(sum(x[r]^2) / cols + eps)
+ *   out[r] = n * weight * (1 + scale[t]) + shift[t]
+ * in fp32, stored once in bf16. x/out are bf16 (rows, cols) with row strides
+ * in elements; weight is (cols,) bf16 or fp32 (w_dtype); scale and shift are
+ * (table_rows, cols) bf16 or fp32 (table_dtype) with their own row strides;
+ * index is int32 or int64 (index_dtype). Indices outside [0, table_rows) are
+ * clamped to the table.
+ */
+typedef struct h3a_rmsnorm_modulate_args {
+    int32_t abi_version;
+    const void *x;
+    void *out;
+    const void *weight;
+    int32_t w_dtype;
+    const void *scale;
+    const void *shift;
+    int32_t table_dtype;
+    int64_t scale_stride;
+    int64_t shift_stride;
+    int64_t table_rows;
+    const void *index;
+    int32_t index_dtype;
+    int64_t n_index;
+    int64_t rows;
+    int64_t cols;
+    int64_t x_stride;
+    int64_t out_stride;
+    float eps;
+} h3a_rmsnorm_modulate_args;
+
+H3A_API int h3a_rmsnorm_modulate(const h3a_rmsnorm_modulate_args *args, void *stream);
+
+/*
+ * Per row r with t = index[r % n_index]:
+ *   h             = residual[r] + gate[t] * branch[r]        (fp32)
+ *   hidden_out[r] = h                                        (bf16)
+ *   n             = h * rsqrt(sum(h^2) / cols + eps) * weight
+ *   normed_out[r] = n * (1 + scale[t]) + shift[t]            (bf16)
+ * The norm uses the unrounded fp32 h. Layouts and dtypes as for
+ * h3a_rmsnorm_modulate; gate is a (table_rows, cols) table like scale.
+ */
+typedef struct h3a_residual_gate_rmsnorm_modulate_args {
+    int32_t abi_version;
+    const void *residual;
+    const void *branch;
+    void *hidden_out;
+    void *normed_out;
+    const void *weight;
+    int32_t w_dtype;
+    const void *gate;
+    const void *scale;
+    const void *shift;
+    int32_t table_dtype;
+    int64_t gate_stride;
+    int64_t scale_stride;
+    int64_t shift_stride;
+    int64_t table_rows;
+    const void *index;
+    int32_t index_dtype;
+    int64_t n_index;
+    int64_t rows;
+    int64_t cols;
+    int64_t residual_stride;
+    int64_t branch_stride;
+    int64_t hidden_stride;
+    int64_t normed_stride;
+    float eps;
+} h3a_residual_gate_rmsnorm_modulate_args;
+
+H3A_API int h3a_residual_gate_rmsnorm_modulate(const h3a_residual_gate_rmsnorm_modulate_args *args, void *stream);
+
+/*
+ * out[r, c] = x[r, c] * (g * sigmoid(g)),  g = x[r, cols + c]
+ * x is bf16 (rows, 2*cols), out bf16 (rows, cols); row strides in elements.
+ */
+typedef struct h3a_swiglu_args {
+    int32_t abi_version;
+    const void *x;
+    void *out;
+    int64_t rows;
+    int64_t cols;
+    int64_t x_stride;
+    int64_t out_stride;
+} h3a_swiglu_args;
+
+H3A_API int h3a_swiglu(const h3a_swiglu_args *args, void *stream);
 
 /* Message of the last failed call on this thread ("" if none). */
 H3A_API const char *h3a_last_error(void);

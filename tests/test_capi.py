@@ -41,6 +41,9 @@ def test_header_declares_the_expected_entry_points():
         "h3a_pack_qkv",
         "h3a_qknorm_rope",
         "h3a_qknorm_rope_pack",
+        "h3a_residual_gate_rmsnorm_modulate",
+        "h3a_rmsnorm_modulate",
+        "h3a_swiglu",
     ]
 
 
@@ -267,3 +270,79 @@ def test_rope_pack_validation(lib, overrides, code, message):
     a = _rope_pack_args(**overrides)
     assert lib.h3a_qknorm_rope_pack(ctypes.byref(a), None) == code
     assert message in _ext.last_error(lib)
+
+
+def _modulate_args(**overrides):
+    a = _ext.RmsnormModulateArgs()
+    a.abi_version = _ext.ABI_VERSION
+    a.x, a.out, a.weight, a.scale, a.shift, a.index = 1 << 20, 1 << 22, 1 << 23, 1 << 24, 1 << 25, 1 << 26
+    a.w_dtype = a.table_dtype = _ext.H3A_DTYPE_BF16
+    a.index_dtype = _ext.H3A_DTYPE_I64
+    a.scale_stride = a.shift_stride = 6 * 512
+    a.table_rows, a.n_index, a.rows, a.cols = 9, 16, 16, 512
+    a.x_stride = a.out_stride = 512
+    a.eps = 1e-5
+    for k, v in overrides.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "overrides, code, message",
+    [
+        ({"abi_version": 0}, _ext.H3A_EINVAL, "abi_version"),
+        ({"cols": 0}, _ext.H3A_EINVAL, "extents"),
+        ({"rows": -3}, _ext.H3A_EINVAL, "extents"),
+        ({"w_dtype": 2}, _ext.H3A_EINVAL, "weight dtype"),
+        ({"table_dtype": 3}, _ext.H3A_EINVAL, "table dtype"),
+        ({"index_dtype": _ext.H3A_DTYPE_F32}, _ext.H3A_EINVAL, "int32 or int64"),
+        ({"n_index": 0}, _ext.H3A_EINVAL, "n_index"),
+        ({"table_rows": 0}, _ext.H3A_EINVAL, "table_rows"),
+        ({"eps": -1.0}, _ext.H3A_EINVAL, "eps"),
+        ({"scale_stride": 100}, _ext.H3A_EINVAL, "table row stride"),
+        ({"x_stride": 100}, _ext.H3A_EINVAL, "x row stride"),
+        ({"shift": None}, _ext.H3A_EINVAL, "NULL"),
+        ({"out": None}, _ext.H3A_EINVAL, "NULL out"),
+    ],
+)
+@host_only
+def test_modulate_validation(lib, overrides, code, message):
+    a = _modulate_args(**overrides)
+    assert lib.h3a_rmsnorm_modulate(ctypes.byref(a), None) == code
+    assert message in _ext.last_error(lib)
+
+
+@host_only
+def test_residual_modulate_validation(lib):
+    a = _ext.ResidualGateRmsnormModulateArgs()
+    a.abi_version = _ext.ABI_VERSION
+    a.residual = a.branch = a.hidden_out = a.normed_out = 1 << 20
+    a.weight = a.gate = a.scale = a.shift = a.index = 1 << 22
+    a.index_dtype = _ext.H3A_DTYPE_I32
+    a.gate_stride = a.scale_stride = a.shift_stride = 64
+    a.table_rows, a.n_index, a.rows, a.cols = 4, 4, 8, 64
+    a.residual_stride = a.branch_stride = a.hidden_stride = a.normed_stride = 64
+    a.gate_stride = 32
+    assert lib.h3a_residual_gate_rmsnorm_modulate(ctypes.byref(a), None) == _ext.H3A_EINVAL
+    assert "table row stride" in _ext.last_error(lib)
+    a.gate_stride, a.hidden_out = 64, None
+    assert lib.h3a_residual_gate_rmsnorm_modulate(ctypes.byref(a), None) == _ext.H3A_EINVAL
+    assert "hidden_out" in _ext.last_error(lib)
+    a.rows = 0
+    a.hidden_out = 1 << 20
+    assert lib.h3a_residual_gate_rmsnorm_modulate(ctypes.byref(a), None) == _ext.H3A_OK
+
+
+@host_only
+def test_swiglu_validation(lib):
+    a = _ext.SwigluArgs()
+    a.abi_version = _ext.ABI_VERSION
+    a.x, a.out = 1 << 20, 1 << 22
+    a.rows, a.cols, a.x_stride, a.out_stride = 4, 64, 100, 64
+    assert lib.h3a_swiglu(ctypes.byref(a), None) == _ext.H3A_EINVAL
+    assert "2*cols" in _ext.last_error(lib)
+    a.x_stride, a.x = 128, None
+    assert lib.h3a_swiglu(ctypes.byref(a), None) == _ext.H3A_EINVAL
+    a.rows = 0
+    assert lib.h3a_swiglu(ctypes.byref(a), None) == _ext.H3A_OK
+    assert lib.h3a_swiglu(None, None) == _ext.H3A_EINVAL
