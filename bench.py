@@ -45,7 +45,7 @@ def parse_args(argv=None):
     p.add_argument("--cpu-rows", type=int, default=0, help="query rows in the CPU baseline sample (0: all)")
     p.add_argument("--cpu-repeats", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--no-relayout", action="store_true", help="skip the packed-Ulysses relayout rates")
+    p.add_argument("--no-relayout", action="store_true", help="skip the packed-Ulysses relayout and row-fusion rates")
     p.add_argument(
         "--copy-calibration",
         type=int,
@@ -176,6 +176,64 @@ def relayout_rates(torch, world: int = 8, heads: int = 40, seqlen: int = 49920, 
         "unfused_prologue_then_pack_ms": unfused_ms,
         "fused_speedup": unfused_ms / fused_ms,
     }
+
+
+def fusion_rates(torch, rows: int = 6240, hidden: int = 5376, ffn: int = 14336) -> dict:
+    """HBM rates of the DiT-block row fusions on one 8-way Ulysses rank's rows
+    at 480p/5s (hidden 5376, ffn 14336, 9 modulation rows), next to the eager
+    torch formulas the reference gates them against
+    (benchmarks/benchmark_transformer_fusions.py:76-105)."""
+
+    from torch.nn import functional
+
+    from h3_flash_amd.fusions import fused_residual_gate_rmsnorm_modulate, fused_rmsnorm_modulate, fused_swiglu
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(17)
+    x = torch.randn((1, rows, hidden), device=dev, generator=g).to(torch.bfloat16)
+    branch = torch.randn_like(x)
+    weight = torch.randn(hidden, device=dev, generator=g).to(torch.bfloat16)
+    wide = torch.randn((9, 6 * hidden), device=dev, generator=g).to(torch.bfloat16)
+    shift_msa, scale_msa, gate_msa, shift_mlp, scale_mlp, _ = wide.chunk(6, -1)
+    idx = torch.arange(rows, device=dev) % 9
+    sw = torch.randn((rows, 2 * ffn), device=dev, generator=g).to(torch.bfloat16)
+    act = rows * hidden * 2
+
+    def eager_first():
+        return functional.rms_norm(x, (hidden,), weight, 1e-5) * (1.0 + scale_msa.index_select(0, idx)) + shift_msa.index_select(0, idx)
+
+    def eager_second():
+        updated = x + gate_msa.index_select(0, idx) * branch
+        normed = functional.rms_norm(updated, (hidden,), weight, 1e-5)
+        return updated, normed * (1.0 + scale_mlp.index_select(0, idx)) + shift_mlp.index_select(0, idx)
+
+    def eager_swiglu():
+        value, gate = sw.chunk(2, -1)
+        return value * functional.silu(gate)
+
+    cases = {
+        "rmsnorm_modulate": (lambda: fused_rmsnorm_modulate(x, weight, scale_msa, shift_msa, idx, 1e-5), eager_first, 2 * act),
+        "residual_gate_rmsnorm_modulate": (
+            lambda: fused_residual_gate_rmsnorm_modulate(x, branch, gate_msa, weight, scale_mlp, shift_mlp, idx, 1e-5),
+            eager_second,
+            4 * act,
+        ),
+        "swiglu": (lambda: fused_swiglu(sw), eager_swiglu, 3 * rows * ffn * 2),
+    }
+    out = {"workload": f"{rows} rows, hidden {hidden}, ffn {ffn}, bf16"}
+    for name, (fused, eager, nbytes) in cases.items():
+        ms = _time_ms(torch, fused)
+        eager_ms = _time_ms(torch, eager)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[name] = {
+            "ms": ms,
+            "bytes_per_launch": nbytes,
+            "GB_s": gbs,
+            "frac_of_hbm_peak": gbs / PEAK_HBM_GBS,
+            "eager_torch_ms": eager_ms,
+            "speedup_vs_eager": eager_ms / ms,
+        }
+    return out
 
 
 def read_pmc_traffic() -> dict | None:
@@ -335,6 +393,7 @@ def main(argv=None) -> int:
         "device": torch.cuda.get_device_name(0),
     }
     result["relayout"] = None if args.no_relayout else relayout_rates(torch)
+    result["fusions"] = None if args.no_relayout else fusion_rates(torch)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, q, k, v, w.heads, args.cpu_rows, args.cpu_repeats)
     else:
