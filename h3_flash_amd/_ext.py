@@ -209,6 +209,31 @@ class SwigluArgs(ctypes.Structure):
     ]
 
 
+H3A_MERGE_MAX_PARTS = 16
+_PtrParts = ctypes.c_void_p * H3A_MERGE_MAX_PARTS
+
+
+class AttnMergeArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("n_parts", ctypes.c_int32),
+        ("o_parts", _PtrParts),
+        ("lse_parts", _PtrParts),
+        ("part_dtype", ctypes.c_int32),
+        ("o", ctypes.c_void_p),
+        ("out_dtype", ctypes.c_int32),
+        ("lse", ctypes.c_void_p),
+        ("batch", ctypes.c_int64),
+        ("heads", ctypes.c_int64),
+        ("seqlen", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("part_o_stride", _I64x3),
+        ("part_lse_stride", _I64x2),
+        ("o_stride", _I64x3),
+        ("lse_stride", _I64x2),
+    ]
+
+
 # Every function the header declares, with its ctypes signature.
 SIGNATURES = {
     "h3a_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
@@ -223,6 +248,7 @@ SIGNATURES = {
         [ctypes.POINTER(ResidualGateRmsnormModulateArgs), ctypes.c_void_p],
     ),
     "h3a_swiglu": (ctypes.c_int, [ctypes.POINTER(SwigluArgs), ctypes.c_void_p]),
+    "h3a_attn_merge": (ctypes.c_int, [ctypes.POINTER(AttnMergeArgs), ctypes.c_void_p]),
     "h3a_last_error": (ctypes.c_char_p, []),
     "h3a_abi_version": (ctypes.c_int, []),
 }

@@ -497,4 +497,52 @@ int h3a_swiglu(const h3a_swiglu_args* a, void* stream) {
     return H3A_OK;
 }
 
+int h3a_attn_merge(const h3a_attn_merge_args* a, void* stream) {
+    g_err[0] = '\0';
+    const char* fn = "h3a_attn_merge";
+    if (a == nullptr) return fail(H3A_EINVAL, "%s: args is NULL", fn);
+    if (a->abi_version != H3A_ABI_VERSION)
+        return fail(H3A_EINVAL, "%s: abi_version %d, library is %d", fn, a->abi_version, H3A_ABI_VERSION);
+    if (a->n_parts < 1 || a->n_parts > H3A_MERGE_MAX_PARTS)
+        return fail(H3A_EINVAL, "%s: n_parts must be in [1, %d], got %d", fn, H3A_MERGE_MAX_PARTS, a->n_parts);
+    if (a->batch < 0 || a->heads <= 0 || a->seqlen < 0 || a->head_dim <= 0)
+        return fail(H3A_EINVAL, "%s: bad extents", fn);
+    if (a->head_dim % 8 != 0 || a->head_dim > 512)
+        return fail(H3A_EUNSUPPORTED, "%s: head_dim must be a multiple of 8 in [8, 512], got %lld", fn, (long long)a->head_dim);
+    const bool pf = a->part_dtype == H3A_DTYPE_F32, of = a->out_dtype == H3A_DTYPE_F32;
+    if ((!pf && a->part_dtype != H3A_DTYPE_BF16) || (!of && a->out_dtype != H3A_DTYPE_BF16))
+        return fail(H3A_EINVAL, "%s: part and out dtypes must be bf16 or fp32", fn);
+    if (a->batch == 0 || a->seqlen == 0) return H3A_OK;
+    if (a->batch * a->seqlen * a->heads >= ((int64_t)1 << 40)) return fail(H3A_EUNSUPPORTED, "%s: too many rows", fn);
+    if (!a->o) return fail(H3A_EINVAL, "%s: NULL output", fn);
+    const int64_t psz = pf ? 4 : 2, osz = of ? 4 : 2;
+    h3a::AttnMergeParams p{};
+    for (int i = 0; i < a->n_parts; ++i) {
+        if (!a->o_parts[i] || !a->lse_parts[i]) return fail(H3A_EINVAL, "%s: NULL part %d", fn, i);
+        if (!aligned16(a->o_parts[i])) return fail(H3A_EINVAL, "%s: part %d must be 16-byte aligned", fn, i);
+        p.o_parts[i] = a->o_parts[i];
+        p.lse_parts[i] = a->lse_parts[i];
+    }
+    for (int d = 0; d < 3; ++d)
+        if (a->part_o_stride[d] < 0 || a->o_stride[d] < 0 || (a->part_o_stride[d] * psz) % 16 != 0 ||
+            (a->o_stride[d] * osz) % 16 != 0)
+            return fail(H3A_EINVAL, "%s: output strides must be non-negative and keep rows 16-byte aligned", fn);
+    if (!aligned16(a->o)) return fail(H3A_EINVAL, "%s: out must be 16-byte aligned", fn);
+    p.o = a->o;
+    p.lse = a->lse;
+    p.po_sb = a->part_o_stride[0]; p.po_ss = a->part_o_stride[1]; p.po_sh = a->part_o_stride[2];
+    p.pl_sb = a->part_lse_stride[0]; p.pl_sh = a->part_lse_stride[1];
+    p.o_sb = a->o_stride[0]; p.o_ss = a->o_stride[1]; p.o_sh = a->o_stride[2];
+    p.l_sb = a->lse_stride[0]; p.l_sh = a->lse_stride[1];
+    p.n_parts = a->n_parts;
+    p.heads = (int32_t)a->heads; p.seqlen = (int32_t)a->seqlen; p.head_dim = (int32_t)a->head_dim;
+    p.rows = a->batch * a->seqlen * a->heads;
+    p.part_f32 = pf; p.out_f32 = of;
+    if (a->seqlen >= ((int64_t)1 << 31) || a->heads >= ((int64_t)1 << 31))
+        return fail(H3A_EUNSUPPORTED, "%s: seqlen and heads must be < 2^31", fn);
+    hipError_t e = h3a::launch_attn_merge(p, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(H3A_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+    return H3A_OK;
+}
+
 }  // extern "C"

@@ -146,4 +146,22 @@ struct SwigluParams {
 };
 hipError_t launch_swiglu(const SwigluParams& p, bool vec, hipStream_t stream);
 
+// LSE merge of partial attention results over disjoint key ranges.
+constexpr int kMergeMaxParts = 16;
+struct AttnMergeParams {
+    const void* o_parts[kMergeMaxParts];
+    const float* lse_parts[kMergeMaxParts];
+    void* o;
+    float* lse;
+    int64_t po_sb, po_ss, po_sh;  // partial outputs (elements)
+    int64_t pl_sb, pl_sh;         // partial LSEs
+    int64_t o_sb, o_ss, o_sh;
+    int64_t l_sb, l_sh;
+    int32_t n_parts;
+    int32_t heads, seqlen, head_dim;
+    int64_t rows;  // batch * seqlen * heads
+    int32_t part_f32, out_f32;
+};
+hipError_t launch_attn_merge(const AttnMergeParams& p, hipStream_t stream);
+
 }  // namespace h3a

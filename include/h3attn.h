@@ -345,6 +345,44 @@ typedef struct h3a_swiglu_args {
 
 H3A_API int h3a_swiglu(const h3a_swiglu_args *args, void *stream);
 
+/*
+ * Merge of partial attention results over disjoint key ranges, the combine
+ * step of ring / context-parallel attention over the (out, lse) pairs that
+ * h3a_attn_fwd returns per key chunk:
+ *   lse = log(sum_p exp(lse_p)),   out = sum_p exp(lse_p - lse) * out_p
+ * in fp32. Parts with lse = -inf weigh nothing; a row with no keys in any
+ * part gets out = 0 and lse = -inf. Partial outputs share one BSHD layout
+ * (part_o_stride) and dtype (bf16 or fp32); partial LSEs share one (B, H, S)
+ * layout. out (bf16 or fp32) and lse may alias part 0 (in-place online
+ * merge). 1 <= n_parts <= 16; head_dim a multiple of 8, at most 512; every
+ * row 16-byte aligned.
+ * No counterpart in the reference's kernels: the FA4 adapter cannot return
+ * the LSE (dense_fa4.py:72-73); this is what a context-parallel forward op
+ * with return_lse=True (dense_fa4.py:53-81) is merged with.
+ */
+#define H3A_MERGE_MAX_PARTS 16
+
+typedef struct h3a_attn_merge_args {
+    int32_t abi_version;
+    int32_t n_parts;
+    const void *o_parts[H3A_MERGE_MAX_PARTS];
+    const float *lse_parts[H3A_MERGE_MAX_PARTS];
+    int32_t part_dtype; /* H3A_DTYPE_BF16 or H3A_DTYPE_F32 */
+    void *o;
+    int32_t out_dtype;  /* H3A_DTYPE_BF16 or H3A_DTYPE_F32 */
+    float *lse;         /* may be NULL */
+    int64_t batch;
+    int64_t heads;
+    int64_t seqlen;
+    int64_t head_dim;
+    int64_t part_o_stride[3];   /* batch, seq, head */
+    int64_t part_lse_stride[2]; /* batch, head */
+    int64_t o_stride[3];
+    int64_t lse_stride[2];
+} h3a_attn_merge_args;
+
+H3A_API int h3a_attn_merge(const h3a_attn_merge_args *args, void *stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 H3A_API const char *h3a_last_error(void);
 

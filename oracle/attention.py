@@ -15,7 +15,7 @@ import torch
 from torch.nn import functional
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
-__all__ = ["sdpa_reference", "sdpa_rows"]
+__all__ = ["merge_reference", "sdpa_reference", "sdpa_rows"]
 
 
 def _dense(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, chunk: int):
@@ -101,4 +101,26 @@ def sdpa_rows(
         a, e = int(offs[s]), int(offs[s + 1])
         o, l = sdpa_reference(qs[:, sel], k[:, a:e], v[:, a:e], scale)
         out[:, sel], lse[:, :, sel] = o, l
+    return out, lse
+
+
+def merge_reference(outs, lses):
+    """fp32 combine of partial attention results over disjoint key ranges:
+    lse = logsumexp_i(lse_i), out = sum_i exp(lse_i - lse) * out_i; parts
+    with lse = -inf weigh nothing, and a row with no keys gets 0 / -inf.
+    outs[i] (B, S, H, D), lses[i] (B, H, S). This is the combine rule of
+    ring / context-parallel attention over a forward op's (out, lse) pairs
+    (src/h3_flash/runtime/attention/dense_fa4.py:53-81 names the op's
+    return_lse argument); it follows from softmax over the union of the key
+    ranges, which tests/test_oracle.py checks against the full attention."""
+
+    L = torch.stack([l.float().cpu() for l in lses])  # (n, B, H, S)
+    O = torch.stack([o.float().cpu() for o in outs])  # (n, B, S, H, D)
+    m = L.max(dim=0).values
+    finite = torch.isfinite(m)
+    w = torch.where(torch.isfinite(L), torch.exp(L - torch.where(finite, m, torch.zeros_like(m))), torch.zeros_like(L))
+    W = w.sum(dim=0)
+    wo = w.permute(0, 1, 3, 2).unsqueeze(-1)  # (n, B, S, H, 1)
+    out = (wo * O).sum(dim=0) / torch.where(W > 0, W, torch.ones_like(W)).permute(0, 2, 1).unsqueeze(-1)
+    lse = torch.where(W > 0, m + torch.log(torch.where(W > 0, W, torch.ones_like(W))), torch.full_like(W, float("-inf")))
     return out, lse

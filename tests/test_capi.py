@@ -36,6 +36,7 @@ def test_header_declares_the_expected_entry_points():
         "h3a_abi_version",
         "h3a_attn_fwd",
         "h3a_attn_fwd_workspace_size",
+        "h3a_attn_merge",
         "h3a_last_error",
         "h3a_merge_heads",
         "h3a_pack_qkv",
@@ -346,3 +347,51 @@ def test_swiglu_validation(lib):
     a.rows = 0
     assert lib.h3a_swiglu(ctypes.byref(a), None) == _ext.H3A_OK
     assert lib.h3a_swiglu(None, None) == _ext.H3A_EINVAL
+
+
+def _attn_merge_args(**overrides):
+    a = _ext.AttnMergeArgs()
+    a.abi_version = _ext.ABI_VERSION
+    a.n_parts = 2
+    a.o_parts[0], a.o_parts[1] = 1 << 20, 1 << 21
+    a.lse_parts[0], a.lse_parts[1] = 1 << 22, 1 << 23
+    a.part_dtype = a.out_dtype = _ext.H3A_DTYPE_BF16
+    a.o, a.lse = 1 << 24, 1 << 25
+    a.batch, a.heads, a.seqlen, a.head_dim = 1, 2, 8, 128
+    a.part_o_stride[:] = a.o_stride[:] = (8 * 2 * 128, 2 * 128, 128)
+    a.part_lse_stride[:] = a.lse_stride[:] = (2 * 8, 8)
+    for k, v in overrides.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "overrides, code, message",
+    [
+        ({"abi_version": 2}, _ext.H3A_EINVAL, "abi_version"),
+        ({"n_parts": 0}, _ext.H3A_EINVAL, "n_parts"),
+        ({"n_parts": 17}, _ext.H3A_EINVAL, "n_parts"),
+        ({"head_dim": 100}, _ext.H3A_EUNSUPPORTED, "multiple of 8"),
+        ({"heads": 0}, _ext.H3A_EINVAL, "extents"),
+        ({"part_dtype": _ext.H3A_DTYPE_I32}, _ext.H3A_EINVAL, "bf16 or fp32"),
+        ({"o": None}, _ext.H3A_EINVAL, "NULL output"),
+        ({"o": (1 << 24) + 8}, _ext.H3A_EINVAL, "aligned"),
+    ],
+)
+@host_only
+def test_attn_merge_validation(lib, overrides, code, message):
+    a = _attn_merge_args(**overrides)
+    assert lib.h3a_attn_merge(ctypes.byref(a), None) == code
+    assert message in _ext.last_error(lib)
+
+
+@host_only
+def test_attn_merge_null_part_and_empty(lib):
+    a = _attn_merge_args()
+    a.lse_parts[1] = None
+    assert lib.h3a_attn_merge(ctypes.byref(a), None) == _ext.H3A_EINVAL
+    assert "NULL part 1" in _ext.last_error(lib)
+    a = _attn_merge_args()
+    a.o_stride[:] = (8 * 2 * 128, 2 * 128, 100)
+    assert lib.h3a_attn_merge(ctypes.byref(a), None) == _ext.H3A_EINVAL
+    assert lib.h3a_attn_merge(ctypes.byref(_attn_merge_args(seqlen=0)), None) == _ext.H3A_OK
