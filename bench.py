@@ -46,6 +46,7 @@ def parse_args(argv=None):
     p.add_argument("--cpu-repeats", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-relayout", action="store_true", help="skip the packed-Ulysses relayout and row-fusion rates")
+    p.add_argument("--no-block", action="store_true", help="skip the whole-attention-block timing")
     p.add_argument(
         "--copy-calibration",
         type=int,
@@ -236,6 +237,80 @@ def fusion_rates(torch, rows: int = 6240, hidden: int = 5376, ffn: int = 14336) 
     return out
 
 
+class _H3Attention:
+    """Random-init stand-in of a MiniMax H3 attention module with the
+    attributes the processor protocol reads (dense_fa4.py:123-133,169-170)."""
+
+    def __init__(self, torch, heads: int, head_dim: int, device) -> None:
+        hidden = heads * head_dim
+        g = torch.Generator(device=device).manual_seed(23)
+
+        def linear(n_in, n_out):
+            lin = torch.nn.Linear(n_in, n_out, bias=True, device=device, dtype=torch.bfloat16)
+            with torch.no_grad():
+                lin.weight.copy_(torch.randn((n_out, n_in), device=device, generator=g) / n_in**0.5)
+                lin.bias.copy_(torch.randn((n_out,), device=device, generator=g) * 0.02)
+            return lin
+
+        self.heads = heads
+        self.fused_projections = False
+        self.to_q, self.to_k, self.to_v = (linear(hidden, hidden) for _ in range(3))
+        self.norm_q = torch.nn.RMSNorm(head_dim, eps=1e-6, device=device, dtype=torch.bfloat16)
+        self.norm_k = torch.nn.RMSNorm(head_dim, eps=1e-6, device=device, dtype=torch.bfloat16)
+        self.to_out = [linear(hidden, hidden), torch.nn.Identity()]
+
+
+def block_rates(torch, heads: int = 40, head_dim: int = 128, grid=(32, 30, 52)) -> dict:
+    """One H3 attention block (projections, q/k RMSNorm + 3D RoPE, attention,
+    out-projection) through the HIP processor, against the reference's eager
+    composition on the same GPU (dense_fa4.py:123-140,169-170 with torch SDPA
+    as at packed_ulysses.py:202-209)."""
+
+    from torch.nn import functional
+
+    from h3_flash_amd import DenseMiniMaxH3Processor
+    from h3_flash_amd.rope import rope_3d_tables
+
+    dev = torch.device("cuda:0")
+    S = grid[0] * grid[1] * grid[2]
+    attn = _H3Attention(torch, heads, head_dim, dev)
+    x = torch.randn((1, S, heads * head_dim), device=dev, generator=torch.Generator(device=dev).manual_seed(29))
+    x = x.to(torch.bfloat16)
+    cos, sin = (t.to(dev) for t in rope_3d_tables(grid))
+    processor = DenseMiniMaxH3Processor()
+
+    def rope_eager(t):  # rotate-half on (B, S, H, D) with (S, D) tables
+        half = t.shape[-1] // 2
+        rot = torch.cat((-t[..., half:], t[..., :half]), dim=-1)
+        return (t.float() * cos[None, :, None, :] + rot.float() * sin[None, :, None, :]).to(t.dtype)
+
+    def eager():
+        q = attn.to_q(x).unflatten(-1, (heads, -1))
+        k = attn.to_k(x).unflatten(-1, (heads, -1))
+        v = attn.to_v(x).unflatten(-1, (heads, -1))
+        q, k = rope_eager(attn.norm_q(q)), rope_eager(attn.norm_k(k))
+        o = functional.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
+        return attn.to_out[0](o.transpose(1, 2).flatten(2, 3))
+
+    def ours():
+        return processor(attn, x, (cos, sin))
+
+    with torch.no_grad():
+        ours_ms = _time_ms(torch, ours, reps=5)
+        eager_ms = _time_ms(torch, eager, reps=3)
+    attn_flop = 4.0 * S * S * head_dim * heads
+    proj_flop = 2.0 * S * (heads * head_dim) ** 2 * 4
+    return {
+        "workload": f"one H3 attention block: B=1 S={S} heads={heads} head_dim={head_dim} hidden={heads * head_dim}, "
+        "random-init weights, bf16",
+        "hip_processor_ms": ours_ms,
+        "eager_torch_sdpa_ms": eager_ms,
+        "speedup": eager_ms / ours_ms,
+        "flop_per_block": attn_flop + proj_flop,
+        "hip_processor_TFLOP_s": (attn_flop + proj_flop) / (ours_ms * 1e-3) / 1e12,
+    }
+
+
 def read_pmc_traffic() -> dict | None:
     """HBM bytes per attention launch from the committed rocprofv3 PMC summary."""
 
@@ -394,6 +469,7 @@ def main(argv=None) -> int:
     }
     result["relayout"] = None if args.no_relayout else relayout_rates(torch)
     result["fusions"] = None if args.no_relayout else fusion_rates(torch)
+    result["block"] = None if args.no_block else block_rates(torch)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, q, k, v, w.heads, args.cpu_rows, args.cpu_repeats)
     else:
