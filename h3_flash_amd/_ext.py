@@ -234,23 +234,6 @@ class AttnMergeArgs(ctypes.Structure):
     ]
 
 
-class ProjGemmArgs(ctypes.Structure):
-    _fields_ = [
-        ("abi_version", ctypes.c_int32),
-        ("x", ctypes.c_void_p),
-        ("w", ctypes.c_void_p),
-        ("y", ctypes.c_void_p),
-        ("bias", ctypes.c_void_p),
-        ("bias_dtype", ctypes.c_int32),
-        ("m", ctypes.c_int64),
-        ("n", ctypes.c_int64),
-        ("k", ctypes.c_int64),
-        ("x_stride", ctypes.c_int64),
-        ("w_stride", ctypes.c_int64),
-        ("y_stride", ctypes.c_int64),
-    ]
-
-
 # Every function the header declares, with its ctypes signature.
 SIGNATURES = {
     "h3a_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
@@ -266,7 +249,6 @@ SIGNATURES = {
     ),
     "h3a_swiglu": (ctypes.c_int, [ctypes.POINTER(SwigluArgs), ctypes.c_void_p]),
     "h3a_attn_merge": (ctypes.c_int, [ctypes.POINTER(AttnMergeArgs), ctypes.c_void_p]),
-    "h3a_proj_gemm": (ctypes.c_int, [ctypes.POINTER(ProjGemmArgs), ctypes.c_void_p]),
     "h3a_last_error": (ctypes.c_char_p, []),
     "h3a_abi_version": (ctypes.c_int, []),
 }

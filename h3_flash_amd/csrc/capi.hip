@@ -6,7 +6,6 @@
 #include <stdarg.h>
 #include <stdio.h>
 
-#include <algorithm>
 #include <atomic>
 
 #include "h3attn.h"
@@ -542,41 +541,6 @@ int h3a_attn_merge(const h3a_attn_merge_args* a, void* stream) {
     if (a->seqlen >= ((int64_t)1 << 31) || a->heads >= ((int64_t)1 << 31))
         return fail(H3A_EUNSUPPORTED, "%s: seqlen and heads must be < 2^31", fn);
     hipError_t e = h3a::launch_attn_merge(p, (hipStream_t)stream);
-    if (e != hipSuccess) return fail(H3A_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
-    return H3A_OK;
-}
-
-int h3a_proj_gemm(const h3a_proj_gemm_args* a, void* stream) {
-    g_err[0] = '\0';
-    const char* fn = "h3a_proj_gemm";
-    if (a == nullptr) return fail(H3A_EINVAL, "%s: args is NULL", fn);
-    if (a->abi_version != H3A_ABI_VERSION)
-        return fail(H3A_EINVAL, "%s: abi_version %d, library is %d", fn, a->abi_version, H3A_ABI_VERSION);
-    if (a->m < 0 || a->n <= 0 || a->k <= 0) return fail(H3A_EINVAL, "%s: bad extents", fn);
-    if (a->k % h3a::proj_gemm_tile_k() != 0 || a->n % 8 != 0)
-        return fail(H3A_EUNSUPPORTED, "%s: K must be a multiple of %d and N of 8 (K=%lld N=%lld)", fn,
-                    h3a::proj_gemm_tile_k(), (long long)a->k, (long long)a->n);
-    if (a->m == 0) return H3A_OK;
-    if (!a->x || !a->w || !a->y) return fail(H3A_EINVAL, "%s: NULL tensor pointer", fn);
-    if (!aligned16(a->x) || !aligned16(a->w) || !aligned16(a->y))
-        return fail(H3A_EINVAL, "%s: tensors must be 16-byte aligned", fn);
-    if (a->x_stride < a->k || a->w_stride < a->k || a->y_stride < a->n || a->x_stride % 8 || a->w_stride % 8 ||
-        a->y_stride % 8)
-        return fail(H3A_EINVAL, "%s: row strides must cover the row and be multiples of 8 elements", fn);
-    if (a->bias_dtype != H3A_DTYPE_BF16 && a->bias_dtype != H3A_DTYPE_F32)
-        return fail(H3A_EINVAL, "%s: bias dtype must be bf16 or fp32", fn);
-    const int64_t tm = h3a::proj_gemm_tile_m();
-    if (a->m >= ((int64_t)1 << 31) || a->n >= ((int64_t)1 << 31) ||
-        (int64_t)std::min<int64_t>(a->m, tm) * a->x_stride * 2 >= ((int64_t)1 << 31) ||
-        (int64_t)256 * a->w_stride * 2 >= ((int64_t)1 << 31))
-        return fail(H3A_EUNSUPPORTED, "%s: extents beyond the 32-bit tile addressing", fn);
-    h3a::ProjGemmParams p{};
-    p.x = a->x; p.w = a->w; p.y = a->y; p.bias = a->bias;
-    p.x_rs = a->x_stride * 2; p.w_rs = a->w_stride * 2; p.y_rs = a->y_stride * 2;
-    p.m = (int32_t)a->m; p.n = (int32_t)a->n; p.k = (int32_t)a->k;
-    p.m_tiles = (int32_t)((a->m + tm - 1) / tm);
-    p.bias_f32 = a->bias_dtype == H3A_DTYPE_F32;
-    hipError_t e = h3a::launch_proj_gemm(p, (hipStream_t)stream);
     if (e != hipSuccess) return fail(H3A_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
     return H3A_OK;
 }

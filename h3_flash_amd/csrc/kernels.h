@@ -164,19 +164,4 @@ struct AttnMergeParams {
 };
 hipError_t launch_attn_merge(const AttnMergeParams& p, hipStream_t stream);
 
-// Projection GEMM Y = X W^T (+ bias). Byte row strides.
-struct ProjGemmParams {
-    const void* x;
-    const void* w;
-    void* y;
-    const void* bias;
-    int64_t x_rs, w_rs, y_rs;
-    int32_t m, n, k;
-    int32_t m_tiles;
-    int32_t bias_f32;
-};
-int proj_gemm_tile_m();
-int proj_gemm_tile_k();
-hipError_t launch_proj_gemm(const ProjGemmParams& p, hipStream_t stream);
-
 }  // namespace h3a

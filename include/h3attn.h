@@ -383,30 +383,6 @@ typedef struct h3a_attn_merge_args {
 
 H3A_API int h3a_attn_merge(const h3a_attn_merge_args *args, void *stream);
 
-/*
- * Projection GEMM y = x w^T (+ bias), the to_q / to_k / to_v / to_out
- * nn.Linear of the attention block (dense_fa4.py:123-128,169-170): x is bf16
- * (m, k), w bf16 (n, k) (the nn.Linear weight), y bf16 (m, n), bias (n,) in
- * bias_dtype or NULL; row strides in elements. fp32 accumulation.
- * k must be a multiple of 32 and n of 8.
- */
-typedef struct h3a_proj_gemm_args {
-    int32_t abi_version;
-    const void *x;
-    const void *w;
-    void *y;
-    const void *bias;
-    int32_t bias_dtype;
-    int64_t m;
-    int64_t n;
-    int64_t k;
-    int64_t x_stride;
-    int64_t w_stride;
-    int64_t y_stride;
-} h3a_proj_gemm_args;
-
-H3A_API int h3a_proj_gemm(const h3a_proj_gemm_args *args, void *stream);
-
 /* Message of the last failed call on this thread ("" if none). */
 H3A_API const char *h3a_last_error(void);
 
