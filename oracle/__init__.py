@@ -16,6 +16,14 @@ Contents and what each follows in the reference repo:
   (max-subtracted exp / sum) for tiny shapes, used to pin the former.
 * ``qknorm_rope.qknorm_rope_reference`` — fp32 restatement of the Triton
   ``_qknorm_partial_rope_kernel`` (src/h3_flash/runtime/kernels/fusions.py:126-175).
+* ``attention.merge_reference`` — fp32 log-sum-exp combine of partial
+  attention results over disjoint key ranges (the context-parallel merge).
+* ``relayout`` — the packed-Ulysses pack / merge movements in two forms, the
+  permute form of src/h3_flash/runtime/parallel/relayout.py:81-94,138-142 and
+  the index arithmetic of its Triton kernels (:28-49, :56-67), plus the
+  all-to-all's effect on the buffers of every rank.
+* ``fusions`` — fp32 restatements of the Triton row fusions
+  (src/h3_flash/runtime/kernels/fusions.py:23-123).
 * ``metrics.error_metrics`` — max_abs / mean_abs / relative_l2 / cosine of
   src/h3_flash/runtime/kernels/transformer.py:16-29 and
   benchmarks/benchmark_dense_fa4.py:92-99.
@@ -28,6 +36,15 @@ How each function is pinned (the checks live in tests/test_oracle.py):
   varlen = concatenation of per-segment dense results; row sampling = rows of
   the full result). Planted mistakes in the oracle fail these checks.
 * attention_fp64: closed forms above, and softmax rows summing to 1.
+* merge_reference: merging the oracle's attention over key chunks equals
+  attention over all keys; empty parts and part order change nothing
+  (tests/test_oracle_merge.py).
+* relayout: the two forms agree on every shape tried, the simulated exchange
+  reproduces the head shards, planted index mistakes fail
+  (tests/test_oracle_relayout.py).
+* fusions: against torch's rms_norm and silu, the reference's eager
+  formulas (benchmarks/benchmark_transformer_fusions.py:76-105) and closed
+  forms; planted mistakes fail (tests/test_oracle_fusions.py).
 * qknorm_rope_reference: against torch.nn.functional.rms_norm (R = 0), the
   complex-multiplication form of rotate-half RoPE, rotation inversion and
   pair-norm preservation, and the golden fixtures.
