@@ -120,19 +120,24 @@ def cpu_baseline(torch, q, k, v, heads, rows: int, repeats: int) -> dict:
 
 
 def _time_ms(torch, fn, reps: int = 20) -> float:
-    """Mean duration of ``fn`` from HIP events on the current stream."""
+    """Mean device time per call of ``fn``: ``reps`` back-to-back calls
+    between two HIP events on the current stream. A spin kernel queued first
+    holds the stream while the host enqueues them, so host-side argument
+    handling never leaves the device idle inside the timed region (kernels of
+    tens of microseconds would otherwise be timed with the host's gaps)."""
 
     for _ in range(3):
         fn()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
-    for a, b in evs:
-        a.record(stream)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda._sleep(20_000_000)
+    a.record(stream)
+    for _ in range(reps):
         fn()
-        b.record(stream)
+    b.record(stream)
     torch.cuda.synchronize()
-    return statistics.fmean(a.elapsed_time(b) for a, b in evs)
+    return a.elapsed_time(b) / reps
 
 
 def relayout_rates(torch, world: int = 8, heads: int = 40, seqlen: int = 49920, head_dim: int = 128) -> dict:
@@ -364,16 +369,7 @@ def main(argv=None) -> int:
             return fused_qk_norm_rope(q_raw, k_raw, wq, wk, cos, sin, raw["eps"], raw["eps"])
 
         q, k = run_prologue()
-        for _ in range(3):
-            run_prologue()
-        torch.cuda.synchronize()
-        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(20)]
-        for a, b in evs:
-            a.record(stream)
-            run_prologue()
-            b.record(stream)
-        torch.cuda.synchronize()
-        pro_ms = statistics.fmean(a.elapsed_time(b) for a, b in evs)
+        pro_ms = _time_ms(torch, run_prologue)
         S, H, D, R = w.seqlen, w.heads, w.head_dim, cos.shape[1]
         pro_bytes = 2 * (2 * S * H * D * 2) + 2 * S * R * 4
         prologue = {
