@@ -45,18 +45,6 @@ __device__ __forceinline__ i32x4 pack8(const float* f) {
     return r;
 }
 
-// Eight consecutive values of a bf16 or fp32 vector (16/32-byte aligned).
-__device__ __forceinline__ void load8(const void* base, int64_t idx, bool f32, float* out) {
-    if (f32) {
-        const f32x4 a = *(const f32x4*)((const float*)base + idx);
-        const f32x4 b = *(const f32x4*)((const float*)base + idx + 4);
-        out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
-        out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
-    } else {
-        unpack8(*(const i32x4*)((const uint16_t*)base + idx), out);
-    }
-}
-
 __device__ __forceinline__ float load1(const void* base, int64_t idx, bool f32) {
     return f32 ? ((const float*)base)[idx] : bf16_to_f32(((const uint16_t*)base)[idx]);
 }
@@ -81,46 +69,119 @@ __device__ __forceinline__ float block_sum(float v, float* lds) {
     return s;
 }
 
+// Eight consecutive bf16 (16 bytes) or fp32 (32 bytes) values as loaded,
+// unpacked only when used, so that many loads can be in flight at once.
+template <bool kF32>
+struct Raw8 {
+    i32x4 a;
+    i32x4 b;  // second half of fp32 values; unused for bf16
+};
+
+template <bool kF32>
+__device__ __forceinline__ Raw8<kF32> fetch8(const void* base, int64_t idx) {
+    Raw8<kF32> r;
+    if constexpr (kF32) {
+        r.a = *(const i32x4*)((const float*)base + idx);
+        r.b = *(const i32x4*)((const float*)base + idx + 4);
+    } else {
+        r.a = *(const i32x4*)((const uint16_t*)base + idx);
+    }
+    return r;
+}
+
+template <bool kF32>
+__device__ __forceinline__ void unpack_raw8(const Raw8<kF32>& r, float* out) {
+    if constexpr (kF32) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            out[i] = __int_as_float(r.a[i]);
+            out[4 + i] = __int_as_float(r.b[i]);
+        }
+    } else {
+        unpack8(r.a, out);
+    }
+}
+
 // Vector path: C % 8 == 0, every row and table row 16-byte aligned.
-// NV = vectors of 8 per thread, NV * 8 * kThreads >= C.
-template <int NV, bool kResidual>
+// NV = vectors of 8 per thread, the fewest with NV * 8 * kThreads >= C, so a
+// thread's vectors 0 .. NV-2 always lie inside the row and only the last may
+// not. That one is loaded from the row's last vector instead and dropped.
+// Every load of a phase is then issued without a branch between loads, and
+// all of them are in flight together (a load behind a bounds branch is
+// waited for before the next one is issued). Table dtypes are template
+// arguments for the same reason.
+template <int NV, bool kResidual, bool kTabF32, bool kWF32>
 __global__ __launch_bounds__(kThreads) void modulate_kernel(ModulateParams p) {
     __shared__ float red[kWaves];
     const int64_t row = blockIdx.x;
     const int C = p.cols;
     const int64_t t = table_row(p, row);
+    int col[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) col[k] = (threadIdx.x + k * kThreads) * 8;
+    const bool last = col[NV - 1] < C;  // the last vector lies inside the row
+    if (!last) col[NV - 1] = C - 8;
+
+    const uint16_t* xr = (const uint16_t*)p.x + row * p.x_stride;
+    i32x4 rx[NV];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) rx[k] = __builtin_nontemporal_load((const i32x4*)(xr + col[k]));
     float h[NV][8];
     float ss = 0.f;
+    if constexpr (kResidual) {
+        const uint16_t* rr = (const uint16_t*)p.residual + row * p.residual_stride;
+        i32x4 rres[NV];
+        Raw8<kTabF32> g[NV];
+#pragma unroll
+        for (int k = 0; k < NV; ++k) rres[k] = __builtin_nontemporal_load((const i32x4*)(rr + col[k]));
+#pragma unroll
+        for (int k = 0; k < NV; ++k) g[k] = fetch8<kTabF32>(p.gate, t * p.gate_stride + col[k]);
+        uint16_t* hr = (uint16_t*)p.hidden + row * p.hidden_stride;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            float r[8], b[8], gv[8];
+            unpack8(rres[k], r);
+            unpack8(rx[k], b);
+            unpack_raw8<kTabF32>(g[k], gv);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) h[k][e] = r[e] + gv[e] * b[e];
+            if (k < NV - 1 || last) {
+                __builtin_nontemporal_store(pack8(h[k]), (i32x4*)(hr + col[k]));
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss += h[k][e] * h[k][e];
+            }
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+            unpack8(rx[k], h[k]);
+            if (k < NV - 1 || last)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss += h[k][e] * h[k][e];
+        }
+    }
+    // Weight and table rows are issued before the reduction, so their latency
+    // overlaps it.
+    Raw8<kWF32> w[NV];
+    Raw8<kTabF32> sc[NV], sh[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-        const int c = (threadIdx.x + k * kThreads) * 8;
-        if (c >= C) break;
-        if constexpr (kResidual) {
-            float r[8], br[8], g[8];
-            unpack8(__builtin_nontemporal_load((const i32x4*)((const uint16_t*)p.residual + row * p.residual_stride + c)), r);
-            unpack8(__builtin_nontemporal_load((const i32x4*)((const uint16_t*)p.x + row * p.x_stride + c)), br);
-            load8(p.gate, t * p.gate_stride + c, p.table_f32, g);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) h[k][e] = r[e] + g[e] * br[e];
-            __builtin_nontemporal_store(pack8(h[k]), (i32x4*)((uint16_t*)p.hidden + row * p.hidden_stride + c));
-        } else {
-            unpack8(__builtin_nontemporal_load((const i32x4*)((const uint16_t*)p.x + row * p.x_stride + c)), h[k]);
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss += h[k][e] * h[k][e];
+        w[k] = fetch8<kWF32>(p.weight, col[k]);
+        sc[k] = fetch8<kTabF32>(p.scale, t * p.scale_stride + col[k]);
+        sh[k] = fetch8<kTabF32>(p.shift, t * p.shift_stride + col[k]);
     }
     const float r = rsqrtf(block_sum(ss, red) / (float)C + p.eps);
+    uint16_t* orow = (uint16_t*)p.out + row * p.out_stride;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-        const int c = (threadIdx.x + k * kThreads) * 8;
-        if (c >= C) break;
-        float w[8], sc[8], sh[8], o[8];
-        load8(p.weight, c, p.w_f32, w);
-        load8(p.scale, t * p.scale_stride + c, p.table_f32, sc);
-        load8(p.shift, t * p.shift_stride + c, p.table_f32, sh);
+        if (k == NV - 1 && !last) break;
+        float wv[8], scv[8], shv[8], o[8];
+        unpack_raw8<kWF32>(w[k], wv);
+        unpack_raw8<kTabF32>(sc[k], scv);
+        unpack_raw8<kTabF32>(sh[k], shv);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = h[k][e] * r * w[e] * (1.0f + sc[e]) + sh[e];
-        __builtin_nontemporal_store(pack8(o), (i32x4*)((uint16_t*)p.out + row * p.out_stride + c));
+        for (int e = 0; e < 8; ++e) o[e] = h[k][e] * r * wv[e] * (1.0f + scv[e]) + shv[e];
+        __builtin_nontemporal_store(pack8(o), (i32x4*)(orow + col[k]));
     }
 }
 
@@ -194,21 +255,34 @@ unsigned stride_grid(int64_t work) {
     return (unsigned)(blocks < 65536 ? (blocks > 0 ? blocks : 1) : 65536);
 }
 
-template <bool kResidual>
-hipError_t launch_modulate_t(const ModulateParams& p, bool vec, hipStream_t stream) {
+template <bool kResidual, bool kTabF32, bool kWF32>
+void launch_modulate_vec(const ModulateParams& p, int nv, hipStream_t stream) {
     const dim3 grid((unsigned)p.rows), block(kThreads);
-    if (!vec) {
-        hipLaunchKernelGGL((modulate_elem_kernel<kResidual>), grid, block, 0, stream, p);
-        return hipGetLastError();
-    }
-    const int nv = (int)((p.cols + 8 * kThreads - 1) / (8 * kThreads));
     switch (nv) {
-#define H3A_NV(n) \
-    case n: hipLaunchKernelGGL((modulate_kernel<n, kResidual>), grid, block, 0, stream, p); break;
+#define H3A_NV(n)                                                                                                     \
+    case n:                                                                                                           \
+        hipLaunchKernelGGL((modulate_kernel<n, kResidual, kTabF32, kWF32>), grid, block, 0, stream, p);             \
+        break;
         H3A_NV(1) H3A_NV(2) H3A_NV(3) H3A_NV(4) H3A_NV(5) H3A_NV(6) H3A_NV(7) H3A_NV(8)
 #undef H3A_NV
-        default:
-            hipLaunchKernelGGL((modulate_elem_kernel<kResidual>), grid, block, 0, stream, p);
+    }
+}
+
+template <bool kResidual>
+hipError_t launch_modulate_t(const ModulateParams& p, bool vec, hipStream_t stream) {
+    const int nv = (int)((p.cols + 8 * kThreads - 1) / (8 * kThreads));
+    if (!vec || nv < 1 || nv > 8) {
+        hipLaunchKernelGGL((modulate_elem_kernel<kResidual>), dim3((unsigned)p.rows), dim3(kThreads), 0, stream, p);
+    } else if (p.table_f32) {
+        if (p.w_f32)
+            launch_modulate_vec<kResidual, true, true>(p, nv, stream);
+        else
+            launch_modulate_vec<kResidual, true, false>(p, nv, stream);
+    } else {
+        if (p.w_f32)
+            launch_modulate_vec<kResidual, false, true>(p, nv, stream);
+        else
+            launch_modulate_vec<kResidual, false, false>(p, nv, stream);
     }
     return hipGetLastError();
 }

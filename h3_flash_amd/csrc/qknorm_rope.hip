@@ -27,7 +27,12 @@ FastDiv make_fast_div(uint32_t d) {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kHeadChunk = 8;  // heads per lane group in the fast path
+// Heads per lane group in the fast path. With a copied third tensor a group
+// holds three tensors' rows in flight, and 4 heads (114 VGPRs, 4 waves per
+// SIMD) measured 8% faster than 8 (162 VGPRs, 3 waves) on a Ulysses rank's
+// shard; 2 heads was slower again. Without a copy, 8 is fastest.
+constexpr int kHeadChunk = 8;
+constexpr int kHeadChunkCopy = 4;
 
 __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) { return (__umulhi(n, f.m) + n) >> f.s; }
 
@@ -101,7 +106,7 @@ __device__ __forceinline__ RowRef locate(const QkNormRopeParams& p, uint32_t row
 template <int L, bool kCopy>
 __global__ __launch_bounds__(kThreads, kCopy ? 3 : 4) void qknorm_rope_kernel(QkNormRopeParams p) {
     constexpr int kGroups = kThreads / L;
-    constexpr int kChunk = kHeadChunk;
+    constexpr int kChunk = kCopy ? kHeadChunkCopy : kHeadChunk;
     const int tid = threadIdx.x;
     const int j = tid % L;
     const int s = (int)blockIdx.x * kGroups + tid / L;  // token
@@ -288,7 +293,8 @@ template <int L>
 hipError_t launch_l(const QkNormRopeParams& p, bool fast, hipStream_t stream) {
     if (fast) {
         const int64_t batch = p.rows / ((int64_t)p.seqlen * p.n_tensors * p.heads);
-        const dim3 grid((unsigned)((p.seqlen + kThreads / L - 1) / (kThreads / L)), (unsigned)((p.heads + kHeadChunk - 1) / kHeadChunk),
+        const int chunk = p.xc != nullptr ? kHeadChunkCopy : kHeadChunk;
+        const dim3 grid((unsigned)((p.seqlen + kThreads / L - 1) / (kThreads / L)), (unsigned)((p.heads + chunk - 1) / chunk),
                         (unsigned)batch);
         if (p.xc != nullptr)
             hipLaunchKernelGGL((qknorm_rope_kernel<L, true>), grid, dim3(kThreads), 0, stream, p);
