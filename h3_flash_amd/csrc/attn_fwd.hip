@@ -101,21 +101,34 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     const int l32 = lane & 31;
 
     // Workgroups are dispatched round-robin over the 8 XCDs, workgroup i to
-    // XCD i % 8, and tile i is workgroup i. The 32 workgroups resident on one
-    // XCD at a time are then every 8th of 256 consecutive tiles: query tiles
-    // of one head (two at a head boundary) that share its K/V in the XCD's
-    // L2. Keeping the dispatch order also keeps the XCDs' shares balanced
-    // when tiles are empty: in a packed varlen batch, tiles past a short
-    // segment's end exit at once, and they are spread over all XCDs instead
-    // of filling the shares of a few (a contiguous tile range per XCD ran the
-    // 49,920 + 1,296 two-segment batch at half speed). With a split, the
-    // whole tiles come first and the pieces after them, so the pieces fill
-    // the last round evenly.
+    // XCD i % 8 as its (i / 8)-th. Dense grids are renumbered so that each
+    // XCD runs one contiguous range of tiles: its 32 resident workgroups are
+    // then consecutive query tiles of one head and stream that head's K/V
+    // through the XCD's L2 once per round (0.98 GB of HBM reads per launch at
+    // B=1 H=5 S=49,920; 1.70 GB in dispatch order, at the same speed). With a
+    // split, every XCD runs its share of whole tiles first and then its share
+    // of the pieces, so the pieces fill the last round evenly.
+    // Packed varlen grids keep dispatch order (tile i is workgroup i): their
+    // tiles past a short segment's end exit at once, and in dispatch order
+    // they spread over all XCDs. Contiguous ranges gave a few XCDs nearly
+    // only empty tiles (the 49,920 + 1,296 two-segment batch ran at half
+    // speed).
     const int bid = blockIdx.x;
     int tile = bid, piece = -1;
-    if (p.split_n != 0 && bid >= p.n_full) {
-        piece = bid - p.n_full;
-        tile = p.n_full + piece % p.split_tiles;
+    if (p.cu_q == nullptr) {
+        const int nb = gridDim.x;
+        const int xcd = bid & 7, local = bid >> 3, per = nb >> 3, rem = nb & 7;
+        const int start = xcd * per + min(xcd, rem);  // first tile of this XCD's share
+        tile = start + local;
+        if (p.split_n != 0) {
+            const int full_per = p.n_full >> 3;  // n_full is a multiple of 8
+            if (local < full_per) {
+                tile = xcd * full_per + local;
+            } else {
+                piece = start - xcd * full_per + (local - full_per);
+                tile = p.n_full + piece % p.split_tiles;
+            }
+        }
     }
     const int qt = tile % p.n_qtiles;
     const int rest = tile / p.n_qtiles;
