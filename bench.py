@@ -45,7 +45,7 @@ def parse_args(argv=None):
     p.add_argument("--cpu-rows", type=int, default=0, help="query rows in the CPU baseline sample (0: all)")
     p.add_argument("--cpu-repeats", type=int, default=2)
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--no-relayout", action="store_true", help="skip the packed-Ulysses relayout and row-fusion rates")
+    p.add_argument("--no-relayout", action="store_true", help="skip the relayout, row-fusion and context-parallel merge rates")
     p.add_argument("--no-block", action="store_true", help="skip the whole-attention-block timing")
     p.add_argument(
         "--copy-calibration",
@@ -181,6 +181,32 @@ def relayout_rates(torch, world: int = 8, heads: int = 40, seqlen: int = 49920, 
         "qknorm_rope_pack": rate("qknorm_rope_kernel<16> (grouped output + v copy)", fused_ms, 2 * 3 * elem + table),
         "unfused_prologue_then_pack_ms": unfused_ms,
         "fused_speedup": unfused_ms / fused_ms,
+    }
+
+
+def merge_rates(torch, parts: int = 8, seqlen: int = 49920, heads: int = 5, head_dim: int = 128) -> dict:
+    """HBM rate of the log-sum-exp merge of context-parallel partial results:
+    ``parts`` bf16 outputs and fp32 LSEs of the single-GPU head shard (one
+    per key chunk) combined into one output and LSE."""
+
+    from h3_flash_amd.context_parallel import merge_attention
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(13)
+    outs = [torch.randn((1, seqlen, heads, head_dim), device=dev, generator=g).to(torch.bfloat16) for _ in range(parts)]
+    lses = [torch.randn((1, heads, seqlen), device=dev, generator=g) for _ in range(parts)]
+    out, lse = torch.empty_like(outs[0]), torch.empty_like(lses[0])
+    ms = _time_ms(torch, lambda: merge_attention(outs, lses, out=out, lse=lse))
+    row = seqlen * heads * (head_dim * 2 + 4)  # one bf16 output and its fp32 LSE
+    nbytes = (parts + 1) * row
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {
+        "workload": f"{parts} partial results of B=1 S={seqlen} H={heads} D={head_dim} bf16 + fp32 LSE -> one",
+        "kernel": "attn_merge_parts_kernel<16>",
+        "ms": ms,
+        "bytes_per_launch": nbytes,
+        "GB_s": gbs,
+        "frac_of_hbm_peak": gbs / PEAK_HBM_GBS,
     }
 
 
@@ -465,6 +491,7 @@ def main(argv=None) -> int:
     }
     result["relayout"] = None if args.no_relayout else relayout_rates(torch)
     result["fusions"] = None if args.no_relayout else fusion_rates(torch)
+    result["cp_merge"] = None if args.no_relayout else merge_rates(torch)
     result["block"] = None if args.no_block else block_rates(torch)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, q, k, v, w.heads, args.cpu_rows, args.cpu_repeats)

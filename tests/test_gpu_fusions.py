@@ -61,6 +61,12 @@ def _inputs(rows, hidden, n_table=9, table_dtype=torch.bfloat16, seed=0):
         (17, 1001, torch.bfloat16, torch.float32, torch.int64),  # odd width: element path
         (5, 20000, torch.bfloat16, torch.bfloat16, torch.int64),  # wider than the vector path
         (64, 8, torch.float32, torch.bfloat16, torch.int32),
+        # vector path at other vector counts per lane (2048 columns per vector
+        # step): a last vector held by one lane only, full steps, the widest
+        (9, 2056, torch.bfloat16, torch.float32, torch.int64),
+        (5, 6144, torch.float32, torch.float32, torch.int32),
+        (4, 14344, torch.float32, torch.bfloat16, torch.int64),
+        (3, 16384, torch.bfloat16, torch.bfloat16, torch.int32),
     ],
 )
 def test_rmsnorm_modulate(rows, hidden, table_dtype, wdtype, idtype):
@@ -73,11 +79,19 @@ def test_rmsnorm_modulate(rows, hidden, table_dtype, wdtype, idtype):
 
 
 @pytest.mark.parametrize(
-    "rows, hidden, table_dtype",
-    [(257, 5376, torch.bfloat16), (6240, 5376, torch.bfloat16), (19, 1000, torch.float32), (9, 1003, torch.bfloat16)],
+    "rows, hidden, table_dtype, wdtype",
+    [
+        (257, 5376, torch.bfloat16, torch.bfloat16),
+        (6240, 5376, torch.bfloat16, torch.bfloat16),
+        (19, 1000, torch.float32, torch.bfloat16),
+        (9, 1003, torch.bfloat16, torch.bfloat16),
+        (7, 2056, torch.float32, torch.float32),
+        (3, 16384, torch.bfloat16, torch.float32),
+    ],
 )
-def test_residual_gate_rmsnorm_modulate(rows, hidden, table_dtype):
+def test_residual_gate_rmsnorm_modulate(rows, hidden, table_dtype, wdtype):
     x, branch, weight, (_, _, gate, shift, scale, _) = _inputs(rows, hidden, table_dtype=table_dtype, seed=2 * rows)
+    weight = weight.to(wdtype)
     index = torch.arange(rows) % 9
     hidden_out, normed = fused_residual_gate_rmsnorm_modulate(
         x.to(DEV), branch.to(DEV), gate.to(DEV), weight.to(DEV), scale.to(DEV), shift.to(DEV), index.to(DEV), 1e-6
