@@ -48,6 +48,39 @@ __device__ __forceinline__ f32x2 halves(float x) {
     return f32x2{__uint_as_float(r[0]), __uint_as_float(r[1])};
 }
 
+// DPP lane movement inside rows of 16 lanes (no LDS round trip, unlike
+// ds_bpermute, which is what __shfl / __shfl_xor compile to).
+enum : int {
+    kDppXor1 = 0xB1,          // quad_perm [1,0,3,2]
+    kDppXor2 = 0x4E,          // quad_perm [2,3,0,1]
+    kDppHalfMirror = 0x141,   // lane i <- lane 7 - i within 8
+    kDppMirror = 0x140,       // lane i <- lane 15 - i within 16
+    kDppRor8 = 0x128,         // lane i <- lane (i + 8) mod 16, i.e. i ^ 8
+};
+
+template <int kCtrl>
+__device__ __forceinline__ int dpp(int x) {
+    return __builtin_amdgcn_update_dpp(0, x, kCtrl, 0xF, 0xF, false);
+}
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp(float x) {
+    return __int_as_float(dpp<kCtrl>(__float_as_int(x)));
+}
+
+// Sum over aligned groups of L <= 16 lanes; every lane of a group receives
+// the group's sum. Each step adds the partial sum of a disjoint set of lanes
+// (pairs, quads, then mirrored halves), so all lanes must be active.
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(L == 1 || L == 2 || L == 4 || L == 8 || L == 16, "group of at most 16 lanes");
+    if constexpr (L >= 2) v += dpp<kDppXor1>(v);
+    if constexpr (L >= 4) v += dpp<kDppXor2>(v);
+    if constexpr (L >= 8) v += dpp<kDppHalfMirror>(v);
+    if constexpr (L >= 16) v += dpp<kDppMirror>(v);
+    return v;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }

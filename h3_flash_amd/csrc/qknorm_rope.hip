@@ -119,6 +119,7 @@ __global__ __launch_bounds__(kThreads, kCopy ? 3 : 4) void qknorm_rope_kernel(Qk
     const bool rot = col0 < R;
     const bool first = col0 < half;
     const int src = rot ? (first ? j + half / 8 : j - half / 8) : j;
+    const bool ror8 = R == 8 * L;  // every lane rotary, partner j ^ (L / 2)
     const bool wf = p.w_f32 != 0;
     const float inv_d = 1.0f / (float)D;
     const bool d_pow2 = (D & (D - 1)) == 0;  // then ss * inv_d == ss / D exactly
@@ -141,13 +142,23 @@ __global__ __launch_bounds__(kThreads, kCopy ? 3 : 4) void qknorm_rope_kernel(Qk
         float ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss += xv[e] * xv[e];
+        if constexpr (L <= 16) {
+            ss = group_sum<L>(ss);
+        } else {
 #pragma unroll
-        for (int off = L / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, L);
+            for (int off = L / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, L);
+        }
         const float r = rsqrtf((d_pow2 ? ss * inv_d : ss / (float)D) + eps);
-        // Partner chunk lives in lane src of the same row.
+        // Partner chunk lives in lane src of the same row; with R = D = 128
+        // that is lane j ^ 8 of the 16, a DPP rotation of the row.
         i32x4 praw;
+        if (L == 16 && ror8) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) praw[e] = __shfl(x[e], src, L);
+            for (int e = 0; e < 4; ++e) praw[e] = dpp<kDppRor8>(x[e]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) praw[e] = __shfl(x[e], src, L);
+        }
         if (!on) return;
         float out[8];
         if (rot) {
@@ -258,8 +269,12 @@ __global__ __launch_bounds__(kThreads) void qknorm_rope_generic_kernel(QkNormRop
     float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) ss += xv[e] * xv[e];
+    if constexpr (L <= 16) {
+        ss = group_sum<L>(ss);
+    } else {
 #pragma unroll
-    for (int off = L / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, L);
+        for (int off = L / 2; off > 0; off >>= 1) ss += __shfl_xor(ss, off, L);
+    }
     if (!active) return;
     const float r = rsqrtf(ss / (float)D + (ref.which ? p.eps[1] : p.eps[0]));
     float out[8];

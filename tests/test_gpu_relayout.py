@@ -135,8 +135,9 @@ def test_merge_strided_input():
 
 @pytest.mark.parametrize("R", [128, 96, 0, 42])
 @pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
-def test_fused_prologue_pack_equals_unfused(R, wdtype):
-    rows, heads, D, world = 211, 40, 128, 8
+@pytest.mark.parametrize("heads, world", [(40, 8), (6, 3), (7, 7)])  # whole and partial head chunks
+def test_fused_prologue_pack_equals_unfused(R, wdtype, heads, world):
+    rows, D = 211, 128
     fused = (torch.randn((rows, 3, heads, D), generator=torch.Generator().manual_seed(R)) * 1.5).to(torch.bfloat16)
     fused = fused.to(DEV)
     q, k, v = fused[:, 0], fused[:, 1], fused[:, 2]
