@@ -1,0 +1,71 @@
+"""The hot path captured in a HIP graph (torch.cuda.CUDAGraph), the way a
+serving loop would replay it: the prologue, the attention with its
+split-tail workspace and merge kernel, and a row fusion. Each replay runs on
+new inputs written into the captured buffers by eager work, and must equal
+the eager launches on the same inputs bit for bit (same kernels, same
+launch shapes, deterministic)."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from h3_flash_amd import flash_attn_func
+from h3_flash_amd.context_parallel import merge_attention
+from h3_flash_amd.fusions import fused_rmsnorm_modulate
+from h3_flash_amd.prologue import fused_qk_norm_rope
+from h3_flash_amd.rope import rope_3d_tables
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _fill(tensors, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    for t in tensors:
+        t.copy_(torch.randn(t.shape, device=DEV, generator=g).to(t.dtype))
+
+
+def test_prologue_attention_and_fusion_replay_in_a_graph():
+    S, H, D, C = 4096, 4, 128, 1024  # 64 query tiles: the split-tail path with its workspace
+    q_raw, k_raw, v = (torch.empty((1, S, H, D), dtype=torch.bfloat16, device=DEV) for _ in range(3))
+    x = torch.empty((1, 512, C), dtype=torch.bfloat16, device=DEV)
+    w = torch.ones(D, dtype=torch.bfloat16, device=DEV)
+    wm = torch.empty(C, dtype=torch.bfloat16, device=DEV)
+    table = torch.empty((9, 2 * C), dtype=torch.bfloat16, device=DEV)
+    index = torch.arange(512, device=DEV) % 9
+    cos, sin = (t.to(DEV) for t in rope_3d_tables((4, 32, 32)))
+
+    def step():
+        q, k = fused_qk_norm_rope(q_raw, k_raw, w, w, cos, sin, 1e-5, 1e-5)
+        o1, l1 = flash_attn_func(q, k[:, : S // 2], v[:, : S // 2])
+        o2, l2 = flash_attn_func(q, k[:, S // 2 :], v[:, S // 2 :])
+        o, l = merge_attention([o1, o2], [l1, l2])
+        full, full_lse = flash_attn_func(q, k, v)
+        y = fused_rmsnorm_modulate(x, wm, table[:, :C], table[:, C:], index, 1e-5)
+        return o, l, full, full_lse, y
+
+    _fill([q_raw, k_raw, v, x, wm, table], 0)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = step()
+    torch.cuda.synchronize()
+
+    for replay in range(4):
+        _fill([q_raw, k_raw, v, x, wm, table], 100 + replay)
+        eager = [t.clone() for t in step()]
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, got, want in zip(("merged", "merged_lse", "attn", "lse", "modulate"), captured, eager):
+            assert torch.equal(got, want), f"replay {replay}: {name} differs from the eager launch"
+    # the merge of the two key halves is the full attention within the path's tolerance
+    o, l, full, full_lse, _ = captured
+    assert (o.float() - full.float()).abs().max().item() <= 2e-2
+    assert (l - full_lse).abs().max().item() <= 1e-3
