@@ -88,8 +88,12 @@ def flash_attn_func(
     strides with a contiguous last dimension. ``softmax_scale`` defaults to
     1/sqrt(128). With ``cu_seqlens_q``/``cu_seqlens_k`` (int32, device,
     ``num_segments + 1`` offsets into the sequence dimension, batch 1) the
-    attention is block-diagonal over the packed segments. ``out``/``lse`` may
-    be passed pre-allocated (BSHD bf16 / (B, H, Sq) fp32).
+    attention is block-diagonal over the packed segments; ``max_seqlen_q``
+    must be at least the longest query segment, as in FlashAttention's
+    varlen call (query rows past it are not computed); when omitted it is
+    read from ``cu_seqlens_q``, which synchronises the stream.
+    ``out``/``lse`` may be passed pre-allocated (BSHD bf16 / (B, H, Sq)
+    fp32).
 
     ``split_tail``: when the query tiles of a dense call leave the last round
     of CUs partly idle, that round's tiles run as key-range pieces merged by
