@@ -6,10 +6,12 @@ artefact of the package; the Python side binds it through ctypes.
 
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
 import sys
+import tempfile
 from pathlib import Path
 
 PACKAGE_DIR = Path(__file__).resolve().parent
@@ -48,31 +50,38 @@ def hipcc() -> str:
     return found
 
 
-def build_library(verbose: bool = False, extra_flags: tuple[str, ...] = ()) -> Path:
-    """Compile every HIP source into ``_lib/libh3attn.so`` and return its path.
-
-    The output is written to a temporary name and renamed, so a concurrent
-    reader never sees a half-written library.
-    """
-
-    LIB_DIR.mkdir(parents=True, exist_ok=True)
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [
-        hipcc(),
-        *HIPCC_FLAGS,
-        *extra_flags,
-        f"-I{INCLUDE_DIR}",
-        *(str(CSRC_DIR / name) for name in SOURCES),
-        "-o",
-        str(tmp),
-    ]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     result = subprocess.run(cmd, capture_output=True, text=True)
     if result.returncode != 0:
-        raise RuntimeError(
-            f"hipcc failed ({result.returncode}):\n{result.stdout}\n{result.stderr}"
-        )
+        raise RuntimeError(f"hipcc failed ({result.returncode}):\n{result.stdout}\n{result.stderr}")
+
+
+def build_library(verbose: bool = False, extra_flags: tuple[str, ...] = ()) -> Path:
+    """Compile every HIP source into ``_lib/libh3attn.so`` and return its path.
+
+    The sources compile in parallel to objects in a temporary directory (no
+    device code crosses translation units), then link into the library. The
+    output is written to a temporary name and renamed, so a concurrent reader
+    never sees a half-written library.
+    """
+
+    LIB_DIR.mkdir(parents=True, exist_ok=True)
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    compiler = hipcc()
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    with tempfile.TemporaryDirectory(prefix="h3a_build_") as objdir:
+        objects = [str(Path(objdir) / (Path(name).stem + ".o")) for name in SOURCES]
+        compiles = [
+            [compiler, *flags, *extra_flags, f"-I{INCLUDE_DIR}", "-c", str(CSRC_DIR / name), "-o", obj]
+            for name, obj in zip(SOURCES, objects)
+        ]
+        workers = max(1, min(len(compiles), os.cpu_count() or 1, 8))
+        with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
+            for future in [pool.submit(_run, cmd, verbose) for cmd in compiles]:
+                future.result()
+        _run([compiler, *HIPCC_FLAGS, *extra_flags, *objects, "-o", str(tmp)], verbose)
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 
