@@ -63,6 +63,10 @@ def _random(shape, dtype, seed):
         (11, 8, 64, 4, torch.float32),
         (7, 4, 16, 2, torch.uint8),
         (5, 6, 32, 3, torch.float64),
+        # wide rows: lane groups of 128 and 256 lanes
+        (6, 4, 1024, 4, torch.bfloat16),
+        (5, 4, 2048, 2, torch.bfloat16),
+        (3, 2, 512, 2, torch.float32),
     ],
 )
 def test_pack_bit_exact(rows, heads, head_dim, world, dtype):
