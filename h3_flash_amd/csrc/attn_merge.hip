@@ -18,7 +18,7 @@
 namespace h3a {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 128;  // 128 measured 3% faster than 256 or 512
 constexpr int kBatch = 4;  // part rows in flight per lane (4 measured faster than 8 or 16)
 
 template <int L>
