@@ -40,7 +40,7 @@ def _case(i: int) -> dict:
     }
 
 
-CASES = [_case(i) for i in range(24)]
+CASES = [_case(i) for i in range(40)]
 
 
 def _tensors(c):
