@@ -95,10 +95,12 @@ def flash_attn_func(
     ``out``/``lse`` may be passed pre-allocated (BSHD bf16 / (B, H, Sq)
     fp32).
 
-    ``split_tail``: when the query tiles of a dense call leave the last round
-    of CUs partly idle, that round's tiles run as key-range pieces merged by
-    a second kernel; the workspace comes from torch's stream-ordered caching
-    allocator. ``False`` runs every tile whole (results differ by rounding).
+    ``split_tail``: the tiles of the last round of a dense call run as
+    key-range pieces (taken from a counter as CUs free up when there are
+    more tiles than CUs; statically assigned when a single round would
+    leave most CUs idle), merged by a second kernel; the workspace comes
+    from torch's stream-ordered caching allocator. ``False`` runs every
+    tile whole (results differ by rounding).
 
     Raises RuntimeError for semantics the dense path does not serve (causal,
     GQA) and for a missing library, mirroring dense_fa4.py:19-20,72-73.

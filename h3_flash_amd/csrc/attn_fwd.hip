@@ -52,6 +52,8 @@ constexpr int kTile = kBN * kRow;  // 16384
 constexpr int kLdsBytes = 2 * kStages * kTile;
 constexpr int kDmaPerTile = kBN / (kWaves * 4);  // 4-row DMA loads per wave per tile
 constexpr float kSumLimit = 65536.0f;            // row-sum bound of the fast softmax path
+constexpr int kQueuePieces = 4;                  // key-range pieces per tile of a dynamic tail
+constexpr int kQueueMinKeyTiles = 16;            // fewest key tiles in such a piece
 
 static_assert(kDmaPerTile == 2, "vmcnt accounting below assumes 2 K + 2 V loads per iteration");
 static_assert(kStages == 4, "the pipeline below is unrolled over four stages");
@@ -86,7 +88,10 @@ __device__ __forceinline__ void wait_vmcnt() {
 // DMA loads in flight are waited for explicitly (wait_vmcnt) before it.
 __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
+// One query tile (piece < 0) or one key-range piece of a split tile. All
+// waves of the workgroup call it with the same arguments; it returns with
+// no LDS DMA in flight.
+__device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int piece) {
     __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
     // V stages 0..3 first, then K stages 0..3: with a per-lane base in a VGPR
     // every fragment read offset then fits the 16-bit ds_read immediate.
@@ -94,42 +99,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     char* const kst = smem + kStages * kTile;
     const lds_char* const lds = (const lds_char*)smem;
 
-    const int tid = threadIdx.x;
+    // Opaque per call, so that no lane-derived value is hoisted out of the
+    // piece loop in attn_fwd_kernel and held across it (that cost VGPRs and
+    // spills).
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hi = lane >> 5;  // wave half
     const int l32 = lane & 31;
 
-    // Workgroups are dispatched round-robin over the 8 XCDs, workgroup i to
-    // XCD i % 8 as its (i / 8)-th. Dense grids are renumbered so that each
-    // XCD runs one contiguous range of tiles: its 32 resident workgroups are
-    // then consecutive query tiles of one head and stream that head's K/V
-    // through the XCD's L2 once per round (0.98 GB of HBM reads per launch at
-    // B=1 H=5 S=49,920; 1.70 GB in dispatch order, at the same speed). With a
-    // split, every XCD runs its share of whole tiles first and then its share
-    // of the pieces, so the pieces fill the last round evenly.
-    // Packed varlen grids keep dispatch order (tile i is workgroup i): their
-    // tiles past a short segment's end exit at once, and in dispatch order
-    // they spread over all XCDs. Contiguous ranges gave a few XCDs nearly
-    // only empty tiles (the 49,920 + 1,296 two-segment batch ran at half
-    // speed).
-    const int bid = blockIdx.x;
-    int tile = bid, piece = -1;
-    if (p.cu_q == nullptr) {
-        const int nb = gridDim.x;
-        const int xcd = bid & 7, local = bid >> 3, per = nb >> 3, rem = nb & 7;
-        const int start = xcd * per + min(xcd, rem);  // first tile of this XCD's share
-        tile = start + local;
-        if (p.split_n != 0) {
-            const int full_per = p.n_full >> 3;  // n_full is a multiple of 8
-            if (local < full_per) {
-                tile = xcd * full_per + local;
-            } else {
-                piece = start - xcd * full_per + (local - full_per);
-                tile = p.n_full + piece % p.split_tiles;
-            }
-        }
-    }
     const int qt = tile % p.n_qtiles;
     const int rest = tile / p.n_qtiles;
     const int h = rest % p.heads;
@@ -572,6 +551,68 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     }
 }
 
+// The dynamic tail: the last round's tiles are cut into key-range pieces
+// that the workgroups after the whole tiles take from a counter in the
+// workspace as they free up, so CUs that ran their whole tiles faster (XCD
+// clocks differ) take more of the tail.
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
+    __shared__ int queue_head;
+    // Workgroups are dispatched round-robin over the 8 XCDs, workgroup i to
+    // XCD i % 8 as its (i / 8)-th. Dense grids are renumbered so that each
+    // XCD runs one contiguous range of tiles: its 32 resident workgroups are
+    // then consecutive query tiles of one head and stream that head's K/V
+    // through the XCD's L2 once per round (0.98 GB of HBM reads per launch at
+    // B=1 H=5 S=49,920; 1.70 GB in dispatch order, at the same speed). With a
+    // split, every XCD runs its share of whole tiles first and then its share
+    // of the pieces, so the pieces fill the last round evenly.
+    // Packed varlen grids keep dispatch order (tile i is workgroup i): their
+    // tiles past a short segment's end exit at once, and in dispatch order
+    // they spread over all XCDs. Contiguous ranges gave a few XCDs nearly
+    // only empty tiles (the 49,920 + 1,296 two-segment batch ran at half
+    // speed).
+    const int bid = blockIdx.x;
+    int tile = bid, piece = -1;
+    // With a tail queue, workgroups [n_full, grid) take the pieces of the
+    // last round's tiles from a counter, one at a time.
+    const bool queued = p.queue != nullptr && bid >= p.n_full;
+    if (p.cu_q == nullptr && !queued) {
+        const int nb = p.queue != nullptr ? p.n_full : (int)gridDim.x;
+        const int xcd = bid & 7, local = bid >> 3, per = nb >> 3, rem = nb & 7;
+        const int start = xcd * per + min(xcd, rem);  // first tile of this XCD's share
+        tile = start + local;
+        if (p.split_n != 0) {
+            const int full_per = p.n_full >> 3;  // n_full is a multiple of 8
+            if (local < full_per) {
+                tile = xcd * full_per + local;
+            } else {
+                piece = start - xcd * full_per + (local - full_per);
+                tile = p.n_full + piece % p.split_tiles;
+            }
+        }
+    }
+    // Two call sites: the whole tiles keep a straight-line copy of the tile
+    // code (a single call inside the loop below changed its register
+    // allocation and made it 1-2% slower).
+    if (!queued) {
+        attn_tile(p, tile, piece);
+        return;
+    }
+    for (;;) {
+        if (threadIdx.x == 0) queue_head = atomicAdd(p.queue, 1);
+        __syncthreads();  // also: every wave is done with the previous piece's LDS
+        piece = __builtin_amdgcn_readfirstlane(queue_head);  // uniform: keep it scalar
+        __syncthreads();  // every wave has read queue_head before it is written again
+        if ((unsigned)piece >= (unsigned)(p.split_n * p.split_tiles)) return;
+        attn_tile(p, p.n_full + piece % p.split_tiles, piece);
+    }
+}
+
+// Zeroes the dynamic tail's counter (a kernel, not a memset, so that the
+// launch can be captured in a graph).
+__global__ void attn_queue_reset(int* queue) {
+    if (threadIdx.x == 0) *queue = 0;
+}
+
 // Combines the split_n partial results of each split tile: with weights
 // w_i = exp(lse_i - max lse), O = sum w_i O_i / sum w_i and
 // LSE = max lse + log(sum w_i). 32 rows per workgroup, 8 lanes per row,
@@ -628,37 +669,61 @@ int attn_fwd_block_n() { return kBN; }
 int attn_fwd_row_margin() { return kBM + kBN * (2 * kStages + 2); }
 
 SplitPlan plan_attn_split(int64_t tiles, int64_t key_tiles, int cus) {
-    // Whole rounds of tiles run as they are; the tiles of a partial last
-    // round are cut into n key-range pieces when that shortens the round
-    // (n <= 8, at least one key tile per piece): ceil(rest * n / cus) / n.
-    // The chip is power-bound under this kernel: a last round that keeps 70%
-    // or more of the CUs busy runs at a higher clock and loses little, and
-    // splitting it does not pay for the pieces and the merge.
-    SplitPlan plan{(int32_t)tiles, 0, 0, 0};
+    SplitPlan plan{(int32_t)tiles, 0, 0, 0, 0, 0};
     if (cus < 8 || cus % 8 != 0 || tiles <= 0) return plan;
-    const int64_t full = tiles / cus * cus, rest = tiles - full;
-    if (rest == 0 || rest * 10 >= (int64_t)cus * 7) return plan;
+    const int64_t piece_bytes = (int64_t)kBM * (kD + 1) * (int64_t)sizeof(float);
+    if (tiles > cus) {
+        // Dynamic tail: the whole rounds but the last run as they are; the
+        // last round's tiles become kQueuePieces key-range pieces each, taken
+        // from a counter by cus workgroups (at most) as CUs free up. Pieces
+        // keep at least kQueueMinKeyTiles key tiles, so the pipeline's fill
+        // and drain stay small against a piece.
+        int n = kQueuePieces;
+        while (n > 1 && key_tiles / n < kQueueMinKeyTiles) --n;
+        if (n < 2) return plan;
+        const int64_t full = (tiles - 1) / cus * cus, rest = tiles - full;
+        plan.n_full = (int32_t)full;
+        plan.split_n = n;
+        plan.split_tiles = (int32_t)rest;
+        plan.queue_blocks = (int32_t)(rest * n < cus ? rest * n : cus);
+        plan.queue_offset = ((int64_t)n * rest * piece_bytes + 255) / 256 * 256;
+        plan.workspace_bytes = plan.queue_offset + 256;
+        return plan;
+    }
+    // One partial round: its tiles are cut into n key-range pieces when that
+    // shortens the round (n <= 8, at least one key tile per piece):
+    // ceil(tiles * n / cus) / n. The chip is power-bound under this kernel:
+    // a round that keeps 70% or more of the CUs busy runs at a higher clock
+    // and loses little, and splitting it does not pay for the pieces and the
+    // merge.
+    if (tiles * 10 >= (int64_t)cus * 7) return plan;
     double best = 1.0;
     int best_n = 0;
     for (int n = 2; n <= 8 && n <= key_tiles; ++n) {
-        const double cost = (double)((rest * n + cus - 1) / cus) / n;
+        const double cost = (double)((tiles * n + cus - 1) / cus) / n;
         if (cost < best - 0.05) {
             best = cost;
             best_n = n;
         }
     }
     if (best_n == 0) return plan;
-    plan.n_full = (int32_t)full;
+    plan.n_full = 0;
     plan.split_n = best_n;
-    plan.split_tiles = (int32_t)rest;
-    plan.workspace_bytes = (int64_t)best_n * rest * kBM * (kD + 1) * (int64_t)sizeof(float);
+    plan.split_tiles = (int32_t)tiles;
+    plan.workspace_bytes = (int64_t)best_n * tiles * piece_bytes;
     return plan;
 }
 
 hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
     const int64_t tiles = (int64_t)p.n_qtiles * p.heads * p.n_groups;
     if (tiles <= 0) return hipSuccess;
-    const int64_t blocks = p.split_n ? (int64_t)p.n_full + (int64_t)p.split_n * p.split_tiles : tiles;
+    int64_t blocks = tiles;
+    if (p.queue != nullptr) {
+        hipLaunchKernelGGL(attn_queue_reset, dim3(1), dim3(64), 0, stream, p.queue);
+        blocks = (int64_t)p.n_full + p.queue_blocks;
+    } else if (p.split_n != 0) {
+        blocks = (int64_t)p.n_full + (int64_t)p.split_n * p.split_tiles;
+    }
     hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.split_n == 0) return e;

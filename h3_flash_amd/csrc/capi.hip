@@ -129,7 +129,7 @@ int device_cus() {
 // uniform work).
 h3a::SplitPlan attn_plan(const h3a_attn_args* a, const h3a::AttnParams& p) {
     const int64_t tiles = (int64_t)p.n_qtiles * p.heads * p.n_groups;
-    h3a::SplitPlan none{(int32_t)tiles, 0, 0, 0};
+    h3a::SplitPlan none{(int32_t)tiles, 0, 0, 0, 0, 0};
     if (a->cu_seqlens_q != nullptr) return none;
     const int bn = h3a::attn_fwd_block_n();
     return h3a::plan_attn_split(tiles, (a->seqlen_k + bn - 1) / bn, device_cus());
@@ -203,6 +203,10 @@ int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
         p.split_tiles = plan.split_tiles;
         p.ws_o = (float*)a->workspace;
         p.ws_lse = p.ws_o + (int64_t)plan.split_n * plan.split_tiles * h3a::attn_fwd_block_m() * 128;
+        if (plan.queue_blocks > 0) {
+            p.queue = (int*)((char*)a->workspace + plan.queue_offset);
+            p.queue_blocks = plan.queue_blocks;
+        }
     }
     hipError_t e = h3a::launch_attn_fwd(p, (hipStream_t)stream);
     if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_attn_fwd: launch failed: %s", hipGetErrorString(e));

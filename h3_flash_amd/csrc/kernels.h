@@ -36,11 +36,19 @@ struct AttnParams {
     int32_t split_tiles;
     float* ws_o;    // [split_n * split_tiles][kBM][128]
     float* ws_lse;  // [split_n * split_tiles][kBM]
+    // Dynamic tail (queue != NULL): workgroups [0, n_full) run whole tiles;
+    // the queue_blocks workgroups after them take piece indices
+    // [0, split_n * split_tiles) from *queue, which the launch zeroes, until
+    // the pieces run out. NULL: pieces are assigned statically.
+    int* queue;
+    int32_t queue_blocks;
 };
 
 // How the query tiles of a dense launch are spread over the CUs.
 struct SplitPlan {
     int32_t n_full, split_n, split_tiles;
+    int32_t queue_blocks;   // > 0: dynamic tail with this many workgroups
+    int64_t queue_offset;   // byte offset of the tail counter in the workspace
     int64_t workspace_bytes;
 };
 SplitPlan plan_attn_split(int64_t tiles, int64_t key_tiles, int cus);

@@ -90,10 +90,13 @@ extern "C" {
  *
  * Rows with no key (seqlen_k == 0) produce O = 0 and LSE = -inf.
  *
- * Workspace (dense inputs only): when the last round of query tiles keeps
- * less than 70% of the GPU's CUs busy (B=1 H=4 S=4096: 64 tiles of 256 rows
- * on 256 CUs), that round's tiles run as several key-range pieces whose fp32
- * partial results are merged by a second kernel on the same stream. That needs h3a_attn_fwd_workspace_size(args) bytes of
+ * Workspace (dense inputs only): with more query tiles (256 rows of one
+ * head) than the GPU has CUs, the tiles of the last round run as key-range
+ * pieces that workgroups take from a counter in the workspace as CUs free
+ * up; with fewer tiles, when they would keep less than 70% of the CUs busy
+ * (B=1 H=4 S=4096: 64 tiles on 256 CUs), they run as statically assigned
+ * pieces. Either way the fp32 partial results are merged by a second kernel
+ * on the same stream (the counter is zeroed by a small kernel first). That needs h3a_attn_fwd_workspace_size(args) bytes of
  * device memory at `workspace` (256-byte aligned); with a NULL or smaller
  * workspace every tile runs whole. The results differ only by rounding.
  * Calls sharing one workspace must be ordered (same stream).

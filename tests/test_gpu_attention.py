@@ -185,6 +185,27 @@ def test_split_tail_matches_whole_tiles():
         assert_parity(o1.cpu(), l1.cpu(), ref_o, ref_l, ("split", shape))
 
 
+def test_dynamic_tail_matches_whole_tiles():
+    # on a 256-CU part: 320 tiles (256 whole, the last 64 as 4 key-range
+    # pieces each, taken from the tail counter), then 336 tiles over two
+    # batches with a ragged key range (256 whole, 80 in pieces)
+    for B, S, H in ((1, 16384, 5), (2, 6000, 7)):
+        q, k, v = (_rand((B, S, H, 128), 60 + i).to(DEV) for i in range(3))
+        o1, l1 = flash_attn_func(q, k, v)
+        o0, l0 = flash_attn_func(q, k, v, split_tail=False)
+        torch.cuda.synchronize()
+        assert (o1.float() - o0.float()).abs().max().item() <= 8e-3, (B, S, H)
+        assert (l1 - l0).abs().max().item() <= 1e-5, (B, S, H)
+        # and against the oracle on seeded rows of the last tiles (the pieces)
+        rows = torch.randint(S - 2048, S, (64,), generator=torch.Generator().manual_seed(S))
+        ref_o, ref_l = sdpa_rows(q.cpu(), k.cpu(), v.cpu(), rows)
+        got_o, got_l = o1.cpu()[:, rows], l1.cpu()[:, :, rows]
+        assert_parity(got_o, got_l, ref_o, ref_l, ("dynamic tail", B, S, H))
+        # repeated launches reuse the counter: same result every time
+        o2, l2 = flash_attn_func(q, k, v)
+        assert torch.equal(o1, o2) and torch.equal(l1, l2)
+
+
 def test_workspace_plan_on_this_device():
     import ctypes
 
@@ -204,12 +225,16 @@ def test_workspace_plan_on_this_device():
         a.softmax_scale = 0.088
         return lib.h3a_attn_fwd_workspace_size(ctypes.byref(a))
 
-    per_piece = 256 * 129 * 4
+    per_piece = 256 * 129 * 4  # a multiple of 256
     if cus == 256:
-        assert need(1, 49920, 5) == 0  # 975 tiles: last round 81% full, not split
+        # more tiles than CUs: the last round's tiles become 4 pieces each in
+        # the dynamic tail, plus 256 bytes for its counter
+        assert need(1, 49920, 5) == 4 * 207 * per_piece + 256  # 975 tiles: 768 whole
+        assert need(1, 256 * 40, 36) == 4 * 160 * per_piece + 256  # 1440 tiles: 1280 whole
+        assert need(1, 256 * 128, 8) == 4 * 256 * per_piece + 256  # 1024 tiles: 768 whole
+        # one partial round: static pieces when it keeps under 70% of the CUs busy
         assert need(1, 4096, 4) == 4 * 64 * per_piece  # 64 tiles, 4 pieces each
-        assert need(1, 256 * 40, 36) == 3 * 160 * per_piece  # 1440 tiles: 1280 whole, 160 in 3 pieces
-        assert need(1, 256 * 128, 8) == 0  # 1024 tiles: whole rounds
+        assert need(1, 256 * 200, 1) == 0  # 200 tiles (78%): whole
     assert need(1, 64, 1) == 0  # one key tile: nothing to split
 
 
