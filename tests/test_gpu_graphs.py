@@ -1,6 +1,7 @@
 """The hot path captured in a HIP graph (torch.cuda.CUDAGraph), the way a
 serving loop would replay it: the prologue, the attention with its
-split-tail workspace and merge kernel, and a row fusion. Each replay runs on
+split-tail workspace and merge kernel, the attention's dynamic tail (its
+counter is reset by a kernel recorded in the graph), and a row fusion. Each replay runs on
 new inputs written into the captured buffers by eager work, and must equal
 the eager launches on the same inputs bit for bit (same kernels, same
 launch shapes, deterministic)."""
@@ -29,6 +30,8 @@ def _fill(tensors, seed):
 def test_prologue_attention_and_fusion_replay_in_a_graph():
     S, H, D, C = 4096, 4, 128, 1024  # 64 query tiles: the split-tail path with its workspace
     q_raw, k_raw, v = (torch.empty((1, S, H, D), dtype=torch.bfloat16, device=DEV) for _ in range(3))
+    # 320 tiles: the dynamic-tail path (counter reset, queued pieces, merge)
+    q2, k2, v2 = (torch.empty((1, 16384, 5, D), dtype=torch.bfloat16, device=DEV) for _ in range(3))
     x = torch.empty((1, 512, C), dtype=torch.bfloat16, device=DEV)
     w = torch.ones(D, dtype=torch.bfloat16, device=DEV)
     wm = torch.empty(C, dtype=torch.bfloat16, device=DEV)
@@ -43,9 +46,10 @@ def test_prologue_attention_and_fusion_replay_in_a_graph():
         o, l = merge_attention([o1, o2], [l1, l2])
         full, full_lse = flash_attn_func(q, k, v)
         y = fused_rmsnorm_modulate(x, wm, table[:, :C], table[:, C:], index, 1e-5)
-        return o, l, full, full_lse, y
+        tail_o, tail_l = flash_attn_func(q2, k2, v2)
+        return o, l, full, full_lse, y, tail_o, tail_l
 
-    _fill([q_raw, k_raw, v, x, wm, table], 0)
+    _fill([q_raw, k_raw, v, x, wm, table, q2, k2, v2], 0)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -58,14 +62,15 @@ def test_prologue_attention_and_fusion_replay_in_a_graph():
     torch.cuda.synchronize()
 
     for replay in range(4):
-        _fill([q_raw, k_raw, v, x, wm, table], 100 + replay)
+        _fill([q_raw, k_raw, v, x, wm, table, q2, k2, v2], 100 + replay)
         eager = [t.clone() for t in step()]
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
-        for name, got, want in zip(("merged", "merged_lse", "attn", "lse", "modulate"), captured, eager):
+        names = ("merged", "merged_lse", "attn", "lse", "modulate", "tail_attn", "tail_lse")
+        for name, got, want in zip(names, captured, eager):
             assert torch.equal(got, want), f"replay {replay}: {name} differs from the eager launch"
     # the merge of the two key halves is the full attention within the path's tolerance
-    o, l, full, full_lse, _ = captured
+    o, l, full, full_lse = captured[:4]
     assert (o.float() - full.float()).abs().max().item() <= 2e-2
     assert (l - full_lse).abs().max().item() <= 1e-3
