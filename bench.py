@@ -480,6 +480,10 @@ def main(argv=None) -> int:
             if traffic
             else None,
             "kernel": "attn_fwd_kernel",
+            # events around each call: for dense launches with more tiles than
+            # CUs that is attn_queue_reset + attn_fwd_kernel + attn_merge_kernel
+            # (the tail's pieces), all of them part of the attention
+            "kernel_ms_scope": "whole flash_attn_func call on its stream",
             "kernel_ms_mean": kernel_ms,
             "kernel_ms_min": min(launch_ms),
             "algorithmic_flop_per_launch": flops,
