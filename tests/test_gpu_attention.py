@@ -206,6 +206,26 @@ def test_dynamic_tail_matches_whole_tiles():
         assert torch.equal(o1, o2) and torch.equal(l1, l2)
 
 
+def test_dynamic_tail_on_concurrent_streams():
+    # two dynamic-tail launches in flight at once on two streams: each call
+    # has its own workspace and counter, so both equal their serial results
+    ins = [[_rand((1, 16384, 5, 128), 80 + 3 * j + i).to(DEV) for i in range(3)] for j in range(2)]
+    serial = [flash_attn_func(*x) for x in ins]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream() for _ in range(2)]
+    for s_ in streams:
+        s_.wait_stream(torch.cuda.current_stream())
+    results = []
+    for x, s_ in zip(ins, streams):
+        with torch.cuda.stream(s_):
+            results.append(flash_attn_func(*x))
+    for s_ in streams:
+        torch.cuda.current_stream().wait_stream(s_)
+    torch.cuda.synchronize()
+    for (o, l), (so, sl) in zip(results, serial):
+        assert torch.equal(o, so) and torch.equal(l, sl)
+
+
 def test_workspace_plan_on_this_device():
     import ctypes
 
