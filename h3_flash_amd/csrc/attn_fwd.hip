@@ -562,9 +562,9 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // XCD runs one contiguous range of tiles: its 32 resident workgroups are
     // then consecutive query tiles of one head and stream that head's K/V
     // through the XCD's L2 once per round (0.98 GB of HBM reads per launch at
-    // B=1 H=5 S=49,920; 1.70 GB in dispatch order, at the same speed). With a
-    // split, every XCD runs its share of whole tiles first and then its share
-    // of the pieces, so the pieces fill the last round evenly.
+    // B=1 H=5 S=49,920; 1.70 GB in dispatch order, at the same speed). A
+    // static split (fewer tiles than CUs, n_full == 0) gives every workgroup
+    // one piece, each XCD a contiguous range of them.
     // Packed varlen grids keep dispatch order (tile i is workgroup i): their
     // tiles past a short segment's end exit at once, and in dispatch order
     // they spread over all XCDs. Contiguous ranges gave a few XCDs nearly
@@ -581,7 +581,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         const int start = xcd * per + min(xcd, rem);  // first tile of this XCD's share
         tile = start + local;
         if (p.split_n != 0) {
-            const int full_per = p.n_full >> 3;  // n_full is a multiple of 8
+            const int full_per = p.n_full >> 3;  // n_full: 0, or whole rounds of CUs (a multiple of 8)
             if (local < full_per) {
                 tile = xcd * full_per + local;
             } else {
