@@ -26,9 +26,9 @@
 //     sum. The offset mc is the first tile's max; later tiles reduce no max:
 //     the row sum bounds every p, and when it passes 2^16 the offset rises
 //     by the sum's binary exponent and P, O and l are scaled by that power
-//     of two, exactly. A tile that overflows (p = inf: a score more than
-//     ~128 log2 units above the offset) is recomputed from K in global
-//     memory against its exact max.
+//     of two, exactly. A tile whose row sum passes 2^64 (a score more than
+//     ~64 log2 units above the offset, up to p = inf) is recomputed from K
+//     in global memory against its exact max.
 // LDS rows are 256 bytes, unpadded; the 16-byte chunk c of row r is stored at
 // chunk c ^ swz(r), swz(r) = 4*(r & 3) + ((r >> 2) & 3). Both read patterns are
 // then bank-conflict free: the K reads (16 consecutive rows, one chunk) and the
@@ -52,6 +52,10 @@ constexpr int kTile = kBN * kRow;  // 16384
 constexpr int kLdsBytes = 2 * kStages * kTile;
 constexpr int kDmaPerTile = kBN / (kWaves * 4);  // 4-row DMA loads per wave per tile
 constexpr float kSumLimit = 65536.0f;            // row-sum bound of the fast softmax path
+// Row sum past which a tile's softmax is recomputed against its exact max. A
+// p of 2^127 * (2 - 2^-8) or more is finite in fp32 but rounds to inf in bf16,
+// and a rescale by 2^-ex with ex > 126 is subnormal; below 2^64 neither occurs.
+constexpr float kRecomputeLimit = 0x1p64f;
 constexpr int kQueuePieces = 4;                  // key-range pieces per tile of a dynamic tail
 constexpr int kQueueMinKeyTiles = 16;            // fewest key tiles in such a piece
 
@@ -261,7 +265,7 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
         }
     };
 
-    // Redo the softmax of a tile whose exponentials overflowed: S again from
+    // Redo the softmax of a tile whose row sum passed kRecomputeLimit: S again from
     // K in global memory (its LDS stage may already hold a newer tile) and
     // the resident Q, then the exact max of the tile, a new offset at or
     // above it, and O and l rescaled to that offset. Leaves every p <= 1.
@@ -409,7 +413,7 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
             // the next PV adds this tile's P.
             if (__builtin_amdgcn_ballot_w64(lsum > kSumLimit)) {
                 asm volatile("" ::: "memory");  // a real branch
-                if (__builtin_amdgcn_ballot_w64(lsum == INFINITY)) {
+                if (__builtin_amdgcn_ballot_w64(lsum > kRecomputeLimit)) {
                     asm volatile("" ::: "memory");
                     overflow(sm_tile, pout, lsum);
                 }

@@ -102,6 +102,30 @@ def test_softmax_scale_argument():
         assert_parity(out, lse, ref_o, ref_l, scale)
 
 
+@pytest.mark.parametrize("scale", [1e-4, 2.0, 12.0, 60.0])
+def test_extreme_softmax_scales_on_random_data(scale):
+    # Large scales make random scores span hundreds of log2 units: the row-sum
+    # rescale and the overflow recompute run on ordinary data, in whole tiles
+    # and in the pieces of a split tail (64 tiles at S=4096 H=4). The softmax
+    # is then peaked and |O| reaches the scale of v (~4) instead of ~6e-3, so
+    # the bf16 rounding of the output and of P (as in the reference's bf16
+    # FA kernel) sets the error: the bound is relative to the largest |O|
+    # (4 bf16 ulps of it), with relative-L2 and cosine gates and the LSE
+    # within 1e-3 plus 1e-6 of its magnitude.
+    for shape in ((1, 700, 3), (1, 4096, 4)):
+        B, S, H = shape
+        q, k, v = (_rand((B, S, H, 128), 90 + i) for i in range(3))
+        out, lse = run(q, k, v, softmax_scale=scale)
+        ref_o, ref_l = sdpa_reference(q, k, v, scale)
+        m = error_metrics(out.float(), ref_o)
+        peak = max(ref_o.abs().max().item(), 1.0)
+        lse_err = ((lse.double() - ref_l.double()).abs() - 1e-6 * ref_l.double().abs()).max().item()
+        assert m["finite"], (scale, shape)
+        assert m["max_abs"] <= max(ATTN_MAX_ABS, 2 ** -6 * peak), (scale, shape, m)
+        assert m["relative_l2"] <= 4e-3 and m["cosine"] >= 0.99999, (scale, shape, m)
+        assert lse_err <= LSE_MAX_ABS, (scale, shape, lse_err)
+
+
 def test_preallocated_outputs_and_current_stream():
     q, k, v = (_rand((1, 130, 1, 128), s).to(DEV) for s in (8, 9, 10))
     out = torch.empty_like(q)
@@ -168,6 +192,44 @@ def test_score_jump_past_exponent_range():
         out, lse = run(q, k, v)
         ref_o, ref_l = sdpa_reference(q, k, v)
         assert_parity(out, lse, ref_o, ref_l, ("jump", pos))
+
+
+@pytest.mark.parametrize("excess", [20.0, 63.5, 100.0, 127.9986, 140.0])
+def test_one_key_far_above_the_first_tile(excess):
+    # Every query is e0 and every key is zero except key pos = 88.5 * e0, so
+    # the first tile of a key range has max 0 and key pos scores
+    # fl32(88.5 * c) = `excess` log2 units above it, c = fl32(scale * log2 e)
+    # as the library computes it. 20 and 63.5 take the power-of-two rescale;
+    # 100 and up are recomputed against the exact max. 127.9986 gives a p that
+    # is finite in fp32 but rounds to inf in bf16 (log2 p in [127.9972, 128)),
+    # and 140 overflows fp32 itself. The key sits in the second tile of the
+    # whole range (100) and of the second of four key-range pieces (1100).
+    import numpy as np
+
+    S, H = 4096, 4
+    scale = excess / (88.5 * 1.4426950408889634)
+    c = np.float32(np.float32(scale) * np.float32(1.4426950408889634))
+    e = float(np.float32(np.float32(88.5) * c))
+    assert abs(e - excess) < 1e-3
+    if excess == 127.9986:
+        assert 127.9972 < e < 128.0
+    q = torch.zeros((1, S, H, 128), dtype=torch.bfloat16)
+    q[..., 0] = 1.0
+    v = _rand((1, S, H, 128), 31)
+    for pos in (100, 1100):
+        k = torch.zeros((1, S, H, 128), dtype=torch.bfloat16)
+        k[0, pos, :, 0] = 88.5
+        ref_o, ref_l = sdpa_reference(q[:, :1], k, v, scale)
+        ref_o, ref_l = ref_o.expand(1, S, H, 128), ref_l.expand(1, H, S)
+        peak = max(ref_o.abs().max().item(), 1.0)
+        for split in (False, True):
+            out, lse = run(q, k, v, softmax_scale=scale, split_tail=split)
+            m = error_metrics(out.float(), ref_o)
+            lse_err = (lse.double() - ref_l.double()).abs().max().item()
+            tag = (excess, pos, split)
+            assert m["finite"], tag
+            assert m["max_abs"] <= max(ATTN_MAX_ABS, 2 ** -7 * peak), (tag, m)
+            assert lse_err <= LSE_MAX_ABS, (tag, lse_err)
 
 
 def test_split_tail_matches_whole_tiles():
