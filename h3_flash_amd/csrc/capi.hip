@@ -26,6 +26,7 @@ int fail(int code, const char* fmt, ...) {
 constexpr int64_t kMaxSpan = (int64_t)1 << 31;  // buffer offsets are 32-bit
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
 
 // Validates the arguments and fills the launch description (split off);
 // *empty: nothing to launch.
@@ -49,6 +50,8 @@ int prepare_attn(const h3a_attn_args* a, h3a::AttnParams& p, bool* empty) {
         return fail(H3A_EINVAL, "h3a_attn_fwd: NULL tensor pointer");
     if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v) || !aligned16(a->o))
         return fail(H3A_EINVAL, "h3a_attn_fwd: q/k/v/o must be 16-byte aligned");
+    if (a->lse != nullptr && (!aligned4(a->lse) || a->lse_stride[0] < 0 || a->lse_stride[1] < 0))
+        return fail(H3A_EINVAL, "h3a_attn_fwd: lse must be 4-byte aligned with non-negative strides");
     const int64_t* st[4] = {a->q_stride, a->k_stride, a->v_stride, a->o_stride};
     const char* nm[4] = {"q", "k", "v", "o"};
     for (int i = 0; i < 4; ++i) {
@@ -244,6 +247,8 @@ int h3a_qknorm_rope(const h3a_qknorm_rope_args* a, void* stream) {
     if (n == 2 && (!a->yk || !a->wk)) return fail(H3A_EINVAL, "h3a_qknorm_rope: xk given without yk/wk");
     if (R > 0 && (!a->cos || !a->sin)) return fail(H3A_EINVAL, "h3a_qknorm_rope: NULL cos/sin table");
     if (R > 0 && a->table_stride < R) return fail(H3A_EINVAL, "h3a_qknorm_rope: table_stride < rotary_dim");
+    if (R > 0 && (!aligned4(a->cos) || !aligned4(a->sin)))
+        return fail(H3A_EINVAL, "h3a_qknorm_rope: cos/sin must be 4-byte aligned");
     h3a::QkNormRopeParams p{};
     const void* xs[2] = {a->xq, a->xk};
     void* ys[2] = {a->yq, a->yk};
@@ -385,6 +390,8 @@ int h3a_qknorm_rope_pack(const h3a_qknorm_rope_pack_args* a, void* stream) {
         return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: NULL tensor pointer");
     if (R > 0 && (!a->cos || !a->sin)) return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: NULL cos/sin table");
     if (R > 0 && a->table_stride < R) return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: table_stride < rotary_dim");
+    if (R > 0 && (!aligned4(a->cos) || !aligned4(a->sin)))
+        return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: cos/sin must be 4-byte aligned");
     const void* ptrs[6] = {a->q, a->k, a->v, a->out, a->wq, a->wk};
     for (const void* q : ptrs)
         if (!aligned16(q)) return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: tensors must be 16-byte aligned");
@@ -524,6 +531,7 @@ int h3a_attn_merge(const h3a_attn_merge_args* a, void* stream) {
     for (int i = 0; i < a->n_parts; ++i) {
         if (!a->o_parts[i] || !a->lse_parts[i]) return fail(H3A_EINVAL, "%s: NULL part %d", fn, i);
         if (!aligned16(a->o_parts[i])) return fail(H3A_EINVAL, "%s: part %d must be 16-byte aligned", fn, i);
+        if (!aligned4(a->lse_parts[i])) return fail(H3A_EINVAL, "%s: LSE of part %d must be 4-byte aligned", fn, i);
         p.o_parts[i] = a->o_parts[i];
         p.lse_parts[i] = a->lse_parts[i];
     }
@@ -532,6 +540,9 @@ int h3a_attn_merge(const h3a_attn_merge_args* a, void* stream) {
             (a->o_stride[d] * osz) % 16 != 0)
             return fail(H3A_EINVAL, "%s: output strides must be non-negative and keep rows 16-byte aligned", fn);
     if (!aligned16(a->o)) return fail(H3A_EINVAL, "%s: out must be 16-byte aligned", fn);
+    if (a->lse != nullptr && !aligned4(a->lse)) return fail(H3A_EINVAL, "%s: lse must be 4-byte aligned", fn);
+    if (a->part_lse_stride[0] < 0 || a->part_lse_stride[1] < 0 || a->lse_stride[0] < 0 || a->lse_stride[1] < 0)
+        return fail(H3A_EINVAL, "%s: LSE strides must be non-negative", fn);
     p.o = a->o;
     p.lse = a->lse;
     p.po_sb = a->part_o_stride[0]; p.po_ss = a->part_o_stride[1]; p.po_sh = a->part_o_stride[2];

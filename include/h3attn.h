@@ -77,8 +77,8 @@ extern "C" {
  *   O = softmax(softmax_scale * Q K^T) V,   LSE = logsumexp(softmax_scale * Q K^T)
  * per (batch, head). Q/K/V/O are bf16 in BSHD layout (batch, seq, head, dim),
  * head_dim must be 128. LSE is fp32, natural log, laid out (batch, head, seq)
- * with strides lse_stride[0] (batch), lse_stride[1] (head) and 1 (seq); it may
- * be NULL when the caller does not want it.
+ * with non-negative strides lse_stride[0] (batch), lse_stride[1] (head) and 1
+ * (seq), 4-byte aligned; it may be NULL when the caller does not want it.
  *
  * Varlen: when cu_seqlens_q is non-NULL, batch must be 1 and the sequence
  * dimension holds `num_segments` packed segments; segment i owns rows
@@ -358,7 +358,7 @@ H3A_API int h3a_swiglu(const h3a_swiglu_args *args, void *stream);
  * (part_o_stride) and dtype (bf16 or fp32); partial LSEs share one (B, H, S)
  * layout. out (bf16 or fp32) and lse may alias part 0 (in-place online
  * merge). 1 <= n_parts <= 16; head_dim a multiple of 8, at most 512; every
- * row 16-byte aligned.
+ * row 16-byte aligned; LSE pointers 4-byte aligned, all strides non-negative.
  * No counterpart in the reference's kernels: the FA4 adapter cannot return
  * the LSE (dense_fa4.py:72-73); this is what a context-parallel forward op
  * with return_lse=True (dense_fa4.py:53-81) is merged with.

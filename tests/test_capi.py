@@ -89,6 +89,8 @@ def _attn_args(**overrides):
         ({"cu_seqlens_q": 1 << 20, "cu_seqlens_k": 1 << 20, "num_segments": 1, "max_seqlen_q": 99},
          _ext.H3A_EINVAL, "max_seqlen_q"),
         ({"seqlen_q": 1 << 23, "seqlen_k": 1 << 23}, _ext.H3A_EUNSUPPORTED, "2^31"),
+        ({"lse": (1 << 20) + 2}, _ext.H3A_EINVAL, "lse must be 4-byte aligned"),
+        ({"lse": 1 << 20, "lse_stride": (ctypes.c_int64 * 2)(-16, 16)}, _ext.H3A_EINVAL, "non-negative strides"),
     ],
 )
 @host_only
@@ -150,6 +152,7 @@ def _rope_args(**overrides):
         ({"xk": 1 << 20}, _ext.H3A_EINVAL, "xk given without"),
         ({"cos": None}, _ext.H3A_EINVAL, "cos/sin"),
         ({"table_stride": 64}, _ext.H3A_EINVAL, "table_stride"),
+        ({"sin": (1 << 21) + 2}, _ext.H3A_EINVAL, "cos/sin must be 4-byte aligned"),
         ({"abi_version": 0}, _ext.H3A_EINVAL, "abi_version"),
     ],
 )
@@ -260,6 +263,7 @@ def _rope_pack_args(**overrides):
         ({"heads": 8, "world": 3}, _ext.H3A_EINVAL, "heads (8) must divide Ulysses degree (3)"),
         ({"rotary_dim": 42}, _ext.H3A_EUNSUPPORTED, "h3a_qknorm_rope then h3a_pack_qkv"),
         ({"cos": (1 << 21) + 4}, _ext.H3A_EUNSUPPORTED, "aligned"),
+        ({"cos": (1 << 21) + 2}, _ext.H3A_EINVAL, "cos/sin must be 4-byte aligned"),
         ({"head_dim": 100, "rotary_dim": 96}, _ext.H3A_EUNSUPPORTED, "multiple of 8"),
         ({"out": None}, _ext.H3A_EINVAL, "NULL"),
         ({"k": (1 << 20) + 2}, _ext.H3A_EINVAL, "aligned"),
@@ -395,3 +399,11 @@ def test_attn_merge_null_part_and_empty(lib):
     a.o_stride[:] = (8 * 2 * 128, 2 * 128, 100)
     assert lib.h3a_attn_merge(ctypes.byref(a), None) == _ext.H3A_EINVAL
     assert lib.h3a_attn_merge(ctypes.byref(_attn_merge_args(seqlen=0)), None) == _ext.H3A_OK
+    a = _attn_merge_args()
+    a.lse_parts[0] = (1 << 22) + 2
+    assert lib.h3a_attn_merge(ctypes.byref(a), None) == _ext.H3A_EINVAL
+    assert "LSE of part 0 must be 4-byte aligned" in _ext.last_error(lib)
+    a = _attn_merge_args()
+    a.part_lse_stride[:] = (-8, 8)
+    assert lib.h3a_attn_merge(ctypes.byref(a), None) == _ext.H3A_EINVAL
+    assert "LSE strides must be non-negative" in _ext.last_error(lib)
