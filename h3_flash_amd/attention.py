@@ -127,12 +127,12 @@ def flash_attn_func(
 
     if out is None:
         out = torch.empty((B, Sq, H, D), dtype=torch.bfloat16, device=q.device)
-    elif out.shape != (B, Sq, H, D) or out.dtype != torch.bfloat16 or out.stride(-1) != 1:
-        raise ValueError("out must be a bf16 (B, Sq, H, 128) tensor with a contiguous last dim")
+    elif out.shape != (B, Sq, H, D) or out.dtype != torch.bfloat16 or out.stride(-1) != 1 or out.device != q.device:
+        raise ValueError(f"out must be a bf16 (B, Sq, H, 128) tensor on {q.device} with a contiguous last dim")
     if lse is None:
         lse = torch.empty((B, H, Sq), dtype=torch.float32, device=q.device)
-    elif lse.shape != (B, H, Sq) or lse.dtype != torch.float32 or lse.stride(-1) != 1:
-        raise ValueError("lse must be an fp32 (B, H, Sq) tensor with a contiguous last dim")
+    elif lse.shape != (B, H, Sq) or lse.dtype != torch.float32 or lse.stride(-1) != 1 or lse.device != q.device:
+        raise ValueError(f"lse must be an fp32 (B, H, Sq) tensor on {q.device} with a contiguous last dim")
 
     args = _ext.AttnArgs()
     args.abi_version = _ext.ABI_VERSION

@@ -89,12 +89,12 @@ def merge_attention(
     out_dtype = out_dtype or (out.dtype if out is not None else dtype)
     if out is None:
         out = torch.empty((B, S, H, D), dtype=out_dtype, device=ref.device)
-    elif out.shape != (B, S, H, D) or out.dtype != out_dtype or out.stride(-1) != 1:
-        raise ValueError("out must be (B, S, H, D) in the requested dtype with a contiguous last dim")
+    elif out.shape != (B, S, H, D) or out.dtype != out_dtype or out.stride(-1) != 1 or out.device != ref.device:
+        raise ValueError(f"out must be (B, S, H, D) in the requested dtype on {ref.device} with a contiguous last dim")
     if lse is None:
         lse = torch.empty((B, H, S), dtype=torch.float32, device=ref.device)
-    elif lse.shape != (B, H, S) or lse.dtype != torch.float32 or lse.stride(-1) != 1:
-        raise ValueError("lse must be fp32 (B, H, S) with a contiguous last dim")
+    elif lse.shape != (B, H, S) or lse.dtype != torch.float32 or lse.stride(-1) != 1 or lse.device != ref.device:
+        raise ValueError(f"lse must be fp32 (B, H, S) on {ref.device} with a contiguous last dim")
     args = _ext.AttnMergeArgs()
     args.abi_version = _ext.ABI_VERSION
     args.n_parts = n

@@ -128,6 +128,8 @@ def fused_residual_gate_rmsnorm_modulate(residual, branch, gate, weight, scale, 
         raise ValueError(f"residual {tuple(residual.shape)} and branch {tuple(branch.shape)} differ")
     residual_flat = _rows(residual, "residual", columns)
     branch_flat = _rows(branch, "branch", columns)
+    if branch.device != residual.device:
+        raise ValueError(f"residual and branch must be on one device, got {residual.device} and {branch.device}")
     weight = _vector(weight, columns, residual.device, "weight")
     gate, scale, shift = _tables([gate, scale, shift], columns, residual.device)
     index = _index(index, residual.device)

@@ -121,6 +121,8 @@ def fused_qk_norm_rope(
         raise ValueError("cos and sin must have the same shape")
     q = _operand(q, "q")
     k = _operand(k, "k")
+    if k.device != q.device:
+        raise ValueError(f"q and k must be on one device, got {q.device} and {k.device}")
     wq = _weight(weight_q, D, q.device)
     wk = _weight(weight_k, D, q.device)
     if wq.dtype != wk.dtype:

@@ -329,6 +329,11 @@ def test_unsupported_requests_raise():
     with pytest.raises(ValueError, match="head_dim"):
         x = _rand((1, 8, 2, 64), 16).to(DEV)
         flash_attn_func(x, x, x)
+    # preallocated outputs on another device are refused before any launch
+    with pytest.raises(ValueError, match="out must be"):
+        flash_attn_func(q, q, q, out=torch.empty((1, 8, 2, 128), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="lse must be"):
+        flash_attn_func(q, q, q, lse=torch.empty((1, 2, 8)))
 
 
 def _prologue_inputs(name):

@@ -109,3 +109,7 @@ def test_merge_errors():
         merge_attention([o], [torch.zeros((1, 2, 5), device=DEV)])
     with pytest.raises(TypeError):
         merge_attention([o.half()], [l])
+    with pytest.raises(ValueError, match="out must be"):
+        merge_attention([o, o], [l, l], out=torch.empty((1, 4, 2, 128), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="lse must be"):
+        merge_attention([o, o], [l, l], lse=torch.empty((1, 2, 4)))
