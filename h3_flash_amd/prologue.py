@@ -54,6 +54,15 @@ def _table(t: torch.Tensor, seqlen: int, device: torch.device) -> torch.Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
+def _tables(cos: torch.Tensor, sin: torch.Tensor, seqlen: int, device: torch.device):
+    """fp32 device cos/sin with one row stride between them (the launch
+    takes a single table stride)."""
+    cos, sin = _table(cos, seqlen, device), _table(sin, seqlen, device)
+    if cos.stride(0) != sin.stride(0):
+        cos, sin = cos.contiguous(), sin.contiguous()
+    return cos, sin
+
+
 def _launch(q, k, wq, wk, cos, sin, eps_q, eps_k, out_q, out_k) -> None:
     B, S, H, D = q.shape
     R = cos.shape[-1]
@@ -94,8 +103,7 @@ def fused_qknorm_rope(
     if sin.shape != cos.shape:
         raise ValueError("cos and sin must have the same shape")
     w = _weight(weight, D, x.device)
-    cos = _table(cos, S, x.device)
-    sin = _table(sin, S, x.device)
+    cos, sin = _tables(cos, sin, S, x.device)
     out = torch.empty((B, S, H, D), dtype=x.dtype, device=x.device)
     _launch(x, None, w, None, cos, sin, eps, eps, out, None)
     return out
@@ -127,8 +135,7 @@ def fused_qk_norm_rope(
     wk = _weight(weight_k, D, q.device)
     if wq.dtype != wk.dtype:
         wq, wk = wq.float(), wk.float()
-    cos = _table(cos, S, q.device)
-    sin = _table(sin, S, q.device)
+    cos, sin = _tables(cos, sin, S, q.device)
     out_q = torch.empty((B, S, H, D), dtype=q.dtype, device=q.device)
     out_k = torch.empty((B, S, H, D), dtype=k.dtype, device=k.device)
     _launch(q, k, wq, wk, cos, sin, eps_q, eps_k, out_q, out_k)

@@ -31,7 +31,7 @@ import torch
 
 from . import _ext
 from .attention import flash_attn_func
-from .prologue import _check_rotary, _table, _weight, fused_qk_norm_rope
+from .prologue import _check_rotary, _tables, _weight, fused_qk_norm_rope
 
 __all__ = [
     "can_pack_qkv",
@@ -177,10 +177,9 @@ def qknorm_rope_pack_qkv(
     wk = _weight(weight_k, head_dim, q.device)
     if wq.dtype != wk.dtype:
         wq, wk = wq.float(), wk.float()
-    cos = _table(cos, rows, q.device)
-    sin = _table(sin, rows, q.device)
+    cos, sin = _tables(cos, sin, rows, q.device)
     aligned = cos.data_ptr() % 16 == 0 and sin.data_ptr() % 16 == 0 and cos.stride(0) % 4 == 0
-    if R % 16 != 0 or not aligned or sin.stride(0) != cos.stride(0):
+    if R % 16 != 0 or not aligned:
         qn, kn = fused_qk_norm_rope(
             q.unsqueeze(0), k.unsqueeze(0), wq, wk, cos, sin, eps_q, eps_k
         )

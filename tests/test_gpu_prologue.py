@@ -98,6 +98,26 @@ def test_strided_input():
     assert_rounding_parity(y, qknorm_rope_reference(q.cpu(), w.cpu(), cos.cpu(), sin.cpu(), 1e-5), "strided")
 
 
+def test_cos_and_sin_with_different_row_strides():
+    # sin as a column slice of a wider table, cos contiguous: one table stride
+    # is passed to the launch, so the wrapper must give both the same stride
+    B, S, H, D, R = 1, 40, 2, 128, 96
+    x = _rand((B, S, H, D), 8)
+    w = torch.ones(D, dtype=torch.bfloat16)
+    ang = torch.randn((S, R), generator=torch.Generator().manual_seed(9))
+    cos = ang.cos()
+    wide = torch.zeros((S, 2 * R))
+    wide[:, R:] = ang.sin()
+    sin = wide[:, R:]
+    assert sin.stride(0) != cos.stride(0)
+    expect = qknorm_rope_reference(x, w, cos, ang.sin(), 1e-5)
+    y = fused_qknorm_rope(x.to(DEV), w.to(DEV), cos.to(DEV), sin.to(DEV), 1e-5)
+    assert_rounding_parity(y, expect, "single")
+    oq, ok = fused_qk_norm_rope(x.to(DEV), x.to(DEV), w.to(DEV), w.to(DEV), cos.to(DEV), sin.to(DEV), 1e-5, 1e-5)
+    assert_rounding_parity(oq, expect, "q")
+    assert_rounding_parity(ok, expect, "k")
+
+
 @pytest.mark.parametrize("name", ["c2", "c5"])
 def test_full_size_workload(name):
     raw = make_raw(WORKLOADS[name])
