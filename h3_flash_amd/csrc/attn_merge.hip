@@ -19,9 +19,16 @@ namespace h3a {
 namespace {
 
 constexpr int kThreads = 128;  // 128 measured 3% faster than 256 or 512
-constexpr int kBatch = 4;  // part rows in flight per lane (4 measured faster than 8 or 16)
 
-template <int L>
+// kPF32: partial outputs are fp32 (else bf16); kMaxP >= n_parts sizes the
+// registers that hold the loaded rows (4, 8 or 16, so a small merge keeps a
+// high occupancy). Every LSE and every part row of the call is loaded in one
+// unrolled sequence before any is used: no load waits behind another's
+// value, and the rows do not wait for the LSEs. The sequence ends on a
+// wave-uniform branch at n_parts; with 16 slots it ends only at a multiple of
+// 4 (the compiler keeps it unrolled then), and a slot past n_parts reloads
+// the last part, dropped by a select.
+template <int L, bool kPF32, int kMaxP>
 __global__ __launch_bounds__(kThreads) void attn_merge_parts_kernel(AttnMergeParams p) {
     const int64_t row = (int64_t)blockIdx.x * (kThreads / L) + threadIdx.x / L;
     const int j = threadIdx.x % L;
@@ -32,60 +39,55 @@ __global__ __launch_bounds__(kThreads) void attn_merge_parts_kernel(AttnMergePar
     const int64_t b = bs / p.seqlen;
     const int64_t lse_off = b * p.pl_sb + h * p.pl_sh + s;
     const int64_t o_off = b * p.po_sb + s * p.po_ss + h * p.po_sh + j * 8;
-    // Every LSE first, then the part rows in batches of kBatch whose loads are
-    // all issued before any is used (a load whose value is used in its own
-    // conditional block is waited for before the next load issues).
-    float lq[kMergeMaxParts];
+    const int n = p.n_parts;
+    constexpr int kStep = kMaxP > 8 ? 4 : 1;  // slots between early exits
+    float lq[kMaxP];
+    i32x4 ra[kMaxP], rb[kPF32 ? kMaxP : 1];
 #pragma unroll
-    for (int q = 0; q < kMergeMaxParts; ++q) lq[q] = q < p.n_parts ? p.lse_parts[q][lse_off] : -INFINITY;
+    for (int q = 0; q < kMaxP; ++q) {
+        if (q % kStep == 0 && q >= n) break;
+        const int qc = q < n ? q : n - 1;
+        lq[q] = p.lse_parts[qc][lse_off];
+        if constexpr (kPF32) {
+            const float* src = (const float*)p.o_parts[qc] + o_off;
+            ra[q] = *(const i32x4*)src;
+            rb[q] = *(const i32x4*)(src + 4);
+        } else {
+            ra[q] = *(const i32x4*)((const uint16_t*)p.o_parts[qc] + o_off);
+        }
+    }
     float m = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < kMergeMaxParts; ++q) m = fmaxf(m, lq[q]);
+    for (int q = 0; q < kMaxP; ++q) {
+        if (q % kStep == 0 && q >= n) break;
+        if (q < n) m = fmaxf(m, lq[q]);
+    }
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float wsum = 0.f;
-    const bool f32 = p.part_f32 != 0;
-    if (m != -INFINITY) {
 #pragma unroll
-        for (int q0 = 0; q0 < kMergeMaxParts; q0 += kBatch) {
-            if (q0 >= p.n_parts) break;
-            i32x4 ra[kBatch], rb[kBatch];
+    for (int q = 0; q < kMaxP; ++q) {
+        if (q % kStep == 0 && q >= n) break;
+        // A part with no keys (lse = -inf), or a reloaded slot, weighs
+        // nothing, and its row (possibly garbage) is replaced by zeros.
+        const bool use = q < n && lq[q] != -INFINITY;
+        const float w = use ? __expf(lq[q] - m) : 0.f;
+        float v[8];
+        if constexpr (kPF32) {
 #pragma unroll
-            for (int i = 0; i < kBatch; ++i) {
-                const int q = q0 + i;
-                if (q < p.n_parts) {
-                    if (f32) {
-                        ra[i] = *(const i32x4*)((const float*)p.o_parts[q] + o_off);
-                        rb[i] = *(const i32x4*)((const float*)p.o_parts[q] + o_off + 4);
-                    } else {
-                        ra[i] = *(const i32x4*)((const uint16_t*)p.o_parts[q] + o_off);
-                    }
-                }
+            for (int e = 0; e < 4; ++e) {
+                v[e] = __int_as_float(ra[q][e]);
+                v[4 + e] = __int_as_float(rb[q][e]);
             }
+        } else {
 #pragma unroll
-            for (int i = 0; i < kBatch; ++i) {
-                const int q = q0 + i;
-                if (q >= p.n_parts) break;
-                if (lq[q] == -INFINITY) continue;
-                const float w = __expf(lq[q] - m);
-                float v[8];
-                if (f32) {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        v[e] = __int_as_float(ra[i][e]);
-                        v[4 + e] = __int_as_float(rb[i][e]);
-                    }
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        v[2 * e] = __uint_as_float(((uint32_t)ra[i][e]) << 16);
-                        v[2 * e + 1] = __uint_as_float(((uint32_t)ra[i][e]) & 0xffff0000u);
-                    }
-                }
-                wsum += w;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) acc[e] += w * v[e];
+            for (int e = 0; e < 4; ++e) {
+                v[2 * e] = __uint_as_float(((uint32_t)ra[q][e]) << 16);
+                v[2 * e + 1] = __uint_as_float(((uint32_t)ra[q][e]) & 0xffff0000u);
             }
         }
+        wsum += w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] = __builtin_fmaf(w, use ? v[e] : 0.f, acc[e]);
     }
     const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
     const int64_t out = b * p.o_sb + s * p.o_ss + h * p.o_sh + j * 8;
@@ -102,25 +104,35 @@ __global__ __launch_bounds__(kThreads) void attn_merge_parts_kernel(AttnMergePar
     if (p.lse != nullptr && j == 0) p.lse[b * p.l_sb + h * p.l_sh + s] = wsum > 0.f ? m + __logf(wsum) : -INFINITY;
 }
 
+template <int L>
+hipError_t launch_l(const AttnMergeParams& p, hipStream_t stream) {
+    const int64_t per = kThreads / L;
+    const dim3 grid((unsigned)((p.rows + per - 1) / per));
+    auto go = [&](auto kernel) {
+        hipLaunchKernelGGL(kernel, grid, dim3(kThreads), 0, stream, p);
+        return hipGetLastError();
+    };
+    const bool f = p.part_f32 != 0;
+    if (p.n_parts <= 4) return f ? go(attn_merge_parts_kernel<L, true, 4>) : go(attn_merge_parts_kernel<L, false, 4>);
+    if (p.n_parts <= 8) return f ? go(attn_merge_parts_kernel<L, true, 8>) : go(attn_merge_parts_kernel<L, false, 8>);
+    return f ? go(attn_merge_parts_kernel<L, true, 16>) : go(attn_merge_parts_kernel<L, false, 16>);
+}
+
 }  // namespace
 
 hipError_t launch_attn_merge(const AttnMergeParams& p, hipStream_t stream) {
     if (p.rows == 0) return hipSuccess;
+    static_assert(kMergeMaxParts == 16, "part-count buckets are 4, 8 and 16");
     int lanes = 1;
     while (lanes * 8 < p.head_dim) lanes <<= 1;
-    auto go = [&](auto kernel, int l) {
-        const int64_t per = kThreads / l;
-        hipLaunchKernelGGL(kernel, dim3((unsigned)((p.rows + per - 1) / per)), dim3(kThreads), 0, stream, p);
-        return hipGetLastError();
-    };
     switch (lanes) {
-        case 1: return go(attn_merge_parts_kernel<1>, 1);
-        case 2: return go(attn_merge_parts_kernel<2>, 2);
-        case 4: return go(attn_merge_parts_kernel<4>, 4);
-        case 8: return go(attn_merge_parts_kernel<8>, 8);
-        case 16: return go(attn_merge_parts_kernel<16>, 16);
-        case 32: return go(attn_merge_parts_kernel<32>, 32);
-        case 64: return go(attn_merge_parts_kernel<64>, 64);
+        case 1: return launch_l<1>(p, stream);
+        case 2: return launch_l<2>(p, stream);
+        case 4: return launch_l<4>(p, stream);
+        case 8: return launch_l<8>(p, stream);
+        case 16: return launch_l<16>(p, stream);
+        case 32: return launch_l<32>(p, stream);
+        case 64: return launch_l<64>(p, stream);
         default: return hipErrorInvalidValue;
     }
 }

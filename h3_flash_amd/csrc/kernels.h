@@ -65,6 +65,7 @@ struct FastDiv {
     uint32_t d, m, s;
 };
 FastDiv make_fast_div(uint32_t d);
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) { return (__umulhi(n, f.m) + n) >> f.s; }
 
 struct QkNormRopeParams {
     const void* x[2];

@@ -34,8 +34,6 @@ constexpr int kThreads = 128;  // 128 measured 1-2% faster than 256 (the pack mo
 constexpr int kHeadChunk = 8;
 constexpr int kHeadChunkCopy = 4;
 
-__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) { return (__umulhi(n, f.m) + n) >> f.s; }
-
 __device__ __forceinline__ void unpack8(i32x4 raw, float* f) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {

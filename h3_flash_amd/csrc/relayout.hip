@@ -22,8 +22,6 @@ namespace {
 
 constexpr int kThreads = 256;
 
-__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) { return (__umulhi(n, f.m) + n) >> f.s; }
-
 // One group of L lanes per (row, head) unit; lane j moves bytes [16j, 16j+16)
 // of the head's row in each of the three tensors.
 // Threads per workgroup of the vector pack: 128 measured 3.5% faster than

@@ -36,7 +36,7 @@ def _partials(n, B=1, S=300, H=5, D=128, dtype=torch.bfloat16, seed=0, empty=())
     return outs, lses
 
 
-@pytest.mark.parametrize("n", [1, 2, 3, 8, 16])
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 8, 13, 16])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_merge_matches_oracle(n, dtype):
     outs, lses = _partials(n, dtype=dtype, seed=n, empty=(1,) if n > 2 else ())
@@ -52,6 +52,19 @@ def test_merge_matches_oracle(n, dtype):
     assert (l.cpu()[finite] - rl[finite]).abs().max().item() <= 1e-5
     if n > 1:
         assert torch.count_nonzero(o[0, 3, 1]) == 0 and l[0, 1, 3].item() == float("-inf")
+
+
+@pytest.mark.parametrize("D", [8, 64, 200, 512])
+@pytest.mark.parametrize("n", [3, 13])
+def test_merge_head_dims(D, n):
+    # lane groups of 1, 8, 32 and 64 lanes (200: the last group is partly idle)
+    outs, lses = _partials(n, S=40, H=3, D=D, dtype=torch.float32, seed=D + n, empty=(1,))
+    o, l = merge_attention([x.to(DEV) for x in outs], [x.to(DEV) for x in lses])
+    ro, rl = merge_reference(outs, lses)
+    torch.testing.assert_close(o.cpu(), ro, rtol=1e-5, atol=1e-6)
+    fin = torch.isfinite(rl)
+    assert torch.equal(torch.isfinite(l.cpu()), fin)
+    assert (l.cpu()[fin] - rl[fin]).abs().max().item() <= 1e-5
 
 
 def test_merge_more_than_sixteen_parts_and_in_place():
