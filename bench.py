@@ -202,7 +202,7 @@ def merge_rates(torch, parts: int = 8, seqlen: int = 49920, heads: int = 5, head
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {
         "workload": f"{parts} partial results of B=1 S={seqlen} H={heads} D={head_dim} bf16 + fp32 LSE -> one",
-        "kernel": "attn_merge_parts_kernel<16>",
+        "kernel": "attn_merge_parts_kernel<16, false, 8>",
         "ms": ms,
         "bytes_per_launch": nbytes,
         "GB_s": gbs,
