@@ -152,6 +152,19 @@ def test_varlen_many_segments_including_empty():
     assert torch.equal(o3.cpu(), out[0]) and torch.equal(l3.cpu(), lse[0])
 
 
+def test_cross_varlen_with_segments_that_have_no_keys():
+    # separate q and k offsets; segments 0 and 2 have queries but no keys
+    cu_q = torch.tensor([0, 5, 70, 300], dtype=torch.int32)
+    cu_k = torch.tensor([0, 0, 100, 100], dtype=torch.int32)
+    q = _rand((1, 300, 2, 128), 41)
+    k, v = _rand((1, 100, 2, 128), 42), _rand((1, 100, 2, 128), 43)
+    out, lse = run(q, k, v, cu_seqlens_q=cu_q.to(DEV), cu_seqlens_k=cu_k.to(DEV))
+    assert torch.all(out[:, :5] == 0) and torch.all(out[:, 70:] == 0)
+    assert torch.all(torch.isneginf(lse[:, :, :5])) and torch.all(torch.isneginf(lse[:, :, 70:]))
+    ref_o, ref_l = sdpa_reference(q[:, 5:70], k, v)
+    assert_parity(out[:, 5:70], lse[:, :, 5:70], ref_o, ref_l, "cross varlen")
+
+
 def test_empty_key_range_gives_zero_and_minus_inf():
     q = _rand((1, 5, 1, 128), 14).to(DEV)
     k = torch.empty((1, 0, 1, 128), dtype=torch.bfloat16, device=DEV)
