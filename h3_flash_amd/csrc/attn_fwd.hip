@@ -620,9 +620,12 @@ __global__ void attn_queue_reset(int* queue) {
 // Combines the split_n partial results of each split tile: with weights
 // w_i = exp(lse_i - max lse), O = sum w_i O_i / sum w_i and
 // LSE = max lse + log(sum w_i). 32 rows per workgroup, 8 lanes per row,
-// 16 head dims per lane.
+// 16 head dims per lane. kMaxP >= split_n sizes the registers of the loaded
+// rows (4 or 8); every LSE and row of the pieces is loaded in one unrolled
+// sequence, ending on a wave-uniform branch at split_n, before any is used.
 constexpr int kMergeRows = 32;
 
+template <int kMaxP>
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
     const int split_tile = blockIdx.x / (kBM / kMergeRows);
     const int row = (blockIdx.x % (kBM / kMergeRows)) * kMergeRows + threadIdx.x / 8;
@@ -634,20 +637,35 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
     const int b = rest / p.heads;
     const int mq = qt * kBM + row;
     if (mq >= p.seqlen_q) return;
+    const int n = p.split_n;
+    float lq[kMaxP];
+    f32x4 part[kMaxP][4];
+#pragma unroll
+    for (int c = 0; c < kMaxP; ++c) {
+        if (c >= n) break;
+        const int64_t pc = (int64_t)c * p.split_tiles + split_tile;
+        lq[c] = p.ws_lse[pc * kBM + row];
+        const f32x4* src = (const f32x4*)(p.ws_o + (pc * kBM + row) * kD + d0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) part[c][i] = src[i];
+    }
     float lse_max = -INFINITY;
-    for (int c = 0; c < p.split_n; ++c)
-        lse_max = fmaxf(lse_max, p.ws_lse[((int64_t)c * p.split_tiles + split_tile) * kBM + row]);
+#pragma unroll
+    for (int c = 0; c < kMaxP; ++c) {
+        if (c >= n) break;
+        lse_max = fmaxf(lse_max, lq[c]);
+    }
     f32x4 acc[4] = {f32x4{}, f32x4{}, f32x4{}, f32x4{}};
     float wsum = 0.f;
-    if (lse_max != -INFINITY) {
-        for (int c = 0; c < p.split_n; ++c) {
-            const int64_t pc = (int64_t)c * p.split_tiles + split_tile;
-            const float w = __expf(p.ws_lse[pc * kBM + row] - lse_max);
-            wsum += w;
-            const f32x4* src = (const f32x4*)(p.ws_o + (pc * kBM + row) * kD + d0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] += w * src[i];
-        }
+    for (int c = 0; c < kMaxP; ++c) {
+        if (c >= n) break;
+        // Every piece holds keys and writes all its rows; a -inf LSE would
+        // still weigh nothing.
+        const float w = lq[c] == -INFINITY ? 0.f : __expf(lq[c] - lse_max);
+        wsum += w;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] += w * part[c][i];
     }
     const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
     char* ob = (char*)p.o + 2 * (b * p.o_sb + h * p.o_sh + d0) + (int64_t)mq * p.o_rs;
@@ -731,8 +749,11 @@ hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
     hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.split_n == 0) return e;
-    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)(p.split_tiles * (kBM / kMergeRows))), dim3(256), 0, stream,
-                       p);
+    const dim3 merge_grid((unsigned)(p.split_tiles * (kBM / kMergeRows)));
+    if (p.split_n <= 4)
+        hipLaunchKernelGGL(attn_merge_kernel<4>, merge_grid, dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL(attn_merge_kernel<8>, merge_grid, dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
