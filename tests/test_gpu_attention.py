@@ -301,6 +301,48 @@ def test_dynamic_tail_on_concurrent_streams():
         assert torch.equal(o, so) and torch.equal(l, sl)
 
 
+def test_small_or_misaligned_workspace_runs_whole_tiles():
+    # through the C ABI: no workspace, one byte short, or not 256-byte
+    # aligned -> every tile runs whole (bit-identical to split_tail=False);
+    # exactly the size asked for -> the split result
+    import ctypes
+    import math
+
+    from h3_flash_amd import _ext
+
+    lib = _ext.load_library()
+    for B, S, H in ((1, 4096, 4), (1, 16384, 5)):
+        q, k, v = (_rand((B, S, H, 128), 70 + i).to(DEV) for i in range(3))
+        whole = flash_attn_func(q, k, v, split_tail=False)
+        split = flash_attn_func(q, k, v)
+
+        def call(offset, short):
+            out = torch.empty_like(q)
+            lse = torch.empty((B, H, S), device=DEV)
+            a = _ext.AttnArgs()
+            a.abi_version = _ext.ABI_VERSION
+            a.q, a.k, a.v, a.o, a.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
+            a.batch, a.heads, a.seqlen_q, a.seqlen_k, a.head_dim = B, H, S, S, 128
+            for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+                getattr(a, name)[:] = (S * H * 128, H * 128, 128)
+            a.lse_stride[:] = (H * S, S)
+            a.softmax_scale = 1.0 / math.sqrt(128)
+            need = lib.h3a_attn_fwd_workspace_size(ctypes.byref(a))
+            assert need > 0
+            ws = torch.empty(need + 512, dtype=torch.uint8, device=DEV)
+            assert ws.data_ptr() % 256 == 0
+            if offset is not None:
+                a.workspace, a.workspace_bytes = ws.data_ptr() + offset, need - short
+            rc = lib.h3a_attn_fwd(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream))
+            assert rc == _ext.H3A_OK, _ext.last_error(lib)
+            torch.cuda.synchronize()
+            return out, lse
+
+        for offset, short, expect in ((None, 0, whole), (0, 1, whole), (16, 0, whole), (0, 0, split)):
+            out, lse = call(offset, short)
+            assert torch.equal(out, expect[0]) and torch.equal(lse, expect[1]), (B, S, H, offset, short)
+
+
 def test_workspace_plan_on_this_device():
     import ctypes
 
