@@ -248,8 +248,14 @@ def hip_forward_op(
 ) -> Any:
     """Forward op with the signature of ``_fa4_forward_op`` (dense_fa4.py:53-81).
 
-    Rejects masks, dropout, GQA and causal attention with RuntimeError; with
-    ``return_lse`` it returns ``(out, lse)`` (lse (B, H, S) fp32).
+    Rejects masks, dropout, GQA and causal attention with RuntimeError. With
+    ``return_lse`` it returns ``(out, lse)`` where ``out`` is (B, S, H, D)
+    and ``lse`` is fp32 **(B, S, H)**: the layout Diffusers' context-parallel
+    template expects from a forward op (its ring merge broadcasts
+    ``lse.unsqueeze(-1)`` against ``out``). The kernel's own (B, H, S) LSE
+    is returned as a transposed view, so no copy is made;
+    :func:`h3_flash_amd.context_parallel.merge_attention` takes it with
+    ``lse_layout="bsh"``.
     """
 
     del _ctx, _save_ctx, _parallel_config
@@ -257,7 +263,8 @@ def hip_forward_op(
         raise RuntimeError("H3 dense HIP attention supports only unmasked non-causal inference attention")
     output = kernel(query, key, value, softmax_scale=scale, causal=False)
     if return_lse:
-        return output
+        out, lse = output
+        return out, lse.transpose(1, 2)
     return output[0] if isinstance(output, tuple) else output
 
 

@@ -44,16 +44,43 @@ def merge_attention(
     out: torch.Tensor | None = None,
     lse: torch.Tensor | None = None,
     out_dtype: torch.dtype | None = None,
+    lse_layout: str = "bhs",
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Combine partial attention results over disjoint key ranges.
 
-    ``outs[i]``: (B, S, H, D) bf16 or fp32, ``lses[i]``: (B, H, S) fp32, as
-    :func:`flash_attn_func` returns them for one key chunk. Returns
-    ``(out, lse)`` with ``lse = logsumexp_i(lses[i])`` and
+    ``outs[i]``: (B, S, H, D) bf16 or fp32. ``lses[i]``: fp32, laid out as
+    ``lse_layout`` says: ``"bhs"`` (B, H, S), as :func:`flash_attn_func`
+    returns it, or ``"bsh"`` (B, S, H), as :func:`hip_forward_op` returns it
+    for Diffusers' context-parallel template. The layout is an explicit
+    argument because the two shapes coincide when S == H. Returns
+    ``(out, lse)`` with ``lse = logsumexp_i(lses[i])`` in the same layout and
     ``out = sum_i exp(lses[i] - lse) * outs[i]``. ``out``/``lse`` may be
     given, and may be ``outs[0]``/``lses[0]`` (in place).
     """
 
+    if lse_layout not in ("bhs", "bsh"):
+        raise ValueError(f"lse_layout must be 'bhs' or 'bsh', got {lse_layout!r}")
+    if lse_layout == "bsh":
+        # (B, S, H) views are (B, H, S) tensors transposed; the launch takes
+        # the (B, H, S) form (a transposed view of a contiguous (B, H, S)
+        # tensor goes back without a copy).
+        for o, l in zip(outs, lses):
+            if l.dim() != 3 or tuple(l.shape) != (o.shape[0], o.shape[1], o.shape[2]):
+                raise ValueError(f"'bsh' LSEs must be (B, S, H) = {tuple(o.shape[:3])}, got {tuple(l.shape)}")
+        if lse is not None and (lse.dim() != 3 or tuple(lse.shape) != tuple(outs[0].shape[:3])):
+            raise ValueError(f"lse must be (B, S, H) = {tuple(outs[0].shape[:3])} with lse_layout='bsh'")
+        direct = lse is not None and lse.transpose(1, 2).stride(-1) == 1
+        o, l = merge_attention(
+            outs,
+            [x.transpose(1, 2) for x in lses],
+            out=out,
+            lse=lse.transpose(1, 2) if direct else None,
+            out_dtype=out_dtype,
+        )
+        if lse is not None and not direct:
+            lse.copy_(l.transpose(1, 2))  # a caller's contiguous (B, S, H) buffer
+            return o, lse
+        return o, l.transpose(1, 2)
     n = len(outs)
     if n == 0 or n != len(lses):
         raise ValueError("merge_attention needs as many LSEs as partial outputs, at least one")

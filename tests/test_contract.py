@@ -1,6 +1,15 @@
-"""CPU contract tests of the adapter, mirroring the reference's
-tests/test_dense_fa4.py:11-52 (fake module + injected fake kernel) plus the
-argument checks of the kernel callable and the prologue."""
+"""CPU contract tests of the adapter and of the kernel callable's argument
+checks.
+
+The processor contract is the one the reference pins in
+tests/test_dense_fa4.py:11-52: with an injected kernel, a (1, 7, 8) hidden
+state over 2 heads reaches the kernel as three (1, 7, 2, 4) BSHD tensors with
+exactly ``causal=False``, the block's output keeps the input shape, the
+``calls`` counter advances by one, and a mask is refused with a "padless"
+message. The fake module here is built for this file: a tiny projection
+stack whose attribute names are the ones the processor protocol reads
+(dense_fa4.py:123-133,169-170).
+"""
 
 from __future__ import annotations
 
@@ -18,18 +27,38 @@ from h3_flash_amd.attention import (
 )
 from h3_flash_amd.prologue import fused_qk_norm_rope, fused_qknorm_rope
 
+HIDDEN, HEADS = 8, 2
 
-class Attention(torch.nn.Module):
-    def __init__(self) -> None:
+
+class TinyH3Block(torch.nn.Module):
+    """Projection stack with the attributes the processor reads; no weights
+    are checked, so they stay at their random initialisation."""
+
+    def __init__(self, fused: bool = False) -> None:
         super().__init__()
-        self.heads = 2
-        self.fused_projections = False
-        self.to_q = torch.nn.Linear(8, 8, bias=False)
-        self.to_k = torch.nn.Linear(8, 8, bias=False)
-        self.to_v = torch.nn.Linear(8, 8, bias=False)
-        self.norm_q = torch.nn.Identity()
-        self.norm_k = torch.nn.Identity()
-        self.to_out = torch.nn.ModuleList([torch.nn.Linear(8, 8, bias=False), torch.nn.Identity()])
+        self.heads = HEADS
+        self.fused_projections = fused
+        if fused:
+            self.to_qkv = torch.nn.Linear(HIDDEN, 3 * HIDDEN, bias=False)
+        for name in ("to_q", "to_k", "to_v"):
+            setattr(self, name, torch.nn.Linear(HIDDEN, HIDDEN, bias=False))
+        self.norm_q, self.norm_k = torch.nn.Identity(), torch.nn.Identity()
+        self.to_out = torch.nn.ModuleList([torch.nn.Linear(HIDDEN, HIDDEN, bias=False), torch.nn.Identity()])
+
+
+class RecordingKernel:
+    """Kernel stand-in: remembers what it was called with and hands back
+    ``v`` (optionally with a dummy LSE, as FA's tuple form does)."""
+
+    def __init__(self, with_lse: bool = False) -> None:
+        self.with_lse = with_lse
+        self.seen: list[tuple[tuple[torch.Size, ...], dict]] = []
+
+    def __call__(self, q, k, v, **kwargs):
+        self.seen.append(((q.shape, k.shape, v.shape), dict(kwargs)))
+        if self.with_lse:
+            return v, torch.zeros(q.shape[0], q.shape[2], q.shape[1])
+        return v
 
 
 def test_missing_library_is_rejected(tmp_path: Path) -> None:
@@ -38,56 +67,50 @@ def test_missing_library_is_rejected(tmp_path: Path) -> None:
 
 
 def test_dense_processor_preserves_shape_and_full_sequence() -> None:
-    seen = {}
-
-    def kernel(q, k, v, **kwargs):
-        seen["shapes"] = (q.shape, k.shape, v.shape)
-        seen["kwargs"] = kwargs
-        return v
-
+    kernel = RecordingKernel()
     processor = DenseMiniMaxH3Processor(kernel=kernel)
-    result = processor(Attention(), torch.randn(1, 7, 8))
+    hidden = torch.randn(1, 7, HIDDEN)
+    block_out = processor(TinyH3Block(), hidden)
 
-    assert result.shape == (1, 7, 8)
-    assert seen["shapes"] == ((1, 7, 2, 4),) * 3
-    assert seen["kwargs"] == {"causal": False}
+    assert block_out.shape == hidden.shape == (1, 7, 8)
+    [(shapes, kwargs)] = kernel.seen  # one kernel call over the whole sequence
+    assert shapes == ((1, 7, 2, 4),) * 3
+    assert kwargs == {"causal": False}
     assert processor.calls == 1
 
 
 def test_dense_processor_takes_first_of_tuple_and_fused_projection() -> None:
-    attn = Attention()
-    attn.fused_projections = True
-    attn.to_qkv = torch.nn.Linear(8, 24, bias=False)
-
-    def kernel(q, k, v, **kwargs):
-        return v, torch.zeros(q.shape[0], q.shape[2], q.shape[1])
-
-    processor = DenseMiniMaxH3Processor(kernel=kernel)
-    x = torch.randn(2, 5, 8)
-    out = processor(attn, x)
-    v = attn.to_qkv(x).chunk(3, dim=-1)[2]
-    assert torch.allclose(out, attn.to_out[0](v))
+    block = TinyH3Block(fused=True)
+    processor = DenseMiniMaxH3Processor(kernel=RecordingKernel(with_lse=True))
+    hidden = torch.randn(2, 5, HIDDEN)
+    block_out = processor(block, hidden)
+    # The kernel echoes v, so the block returns to_out applied to the v third
+    # of the fused projection.
+    value = block.to_qkv(hidden)[..., 2 * HIDDEN :]
+    assert torch.allclose(block_out, block.to_out[0](value))
     assert processor.calls == 1
 
 
 def test_dense_processor_rejects_masked_sequence() -> None:
-    processor = DenseMiniMaxH3Processor(kernel=lambda *args, **kwargs: None)
+    kernel = RecordingKernel()
+    processor = DenseMiniMaxH3Processor(kernel=kernel)
     with pytest.raises(RuntimeError, match="padless"):
-        processor(None, None, attention_mask=object())
+        processor(TinyH3Block(), torch.randn(1, 3, HIDDEN), attention_mask=torch.ones(1, 3, dtype=torch.bool))
+    assert kernel.seen == [] and processor.calls == 0
 
 
 def test_rotary_path_requires_rmsnorm_parameters() -> None:
     processor = DenseMiniMaxH3Processor(kernel=lambda q, k, v, **kw: v)
     cos = torch.ones(7, 4)
     with pytest.raises(RuntimeError, match="norm_q/norm_k"):
-        processor(Attention(), torch.randn(1, 7, 8), rotary_emb=(cos, cos))
+        processor(TinyH3Block(), torch.randn(1, 7, HIDDEN), rotary_emb=(cos, cos))
 
 
 def test_context_parallel_is_refused() -> None:
     processor = DenseMiniMaxH3Processor(kernel=lambda q, k, v, **kw: v)
     processor._parallel_config = object()
     with pytest.raises(RuntimeError, match="head shard"):
-        processor(Attention(), torch.randn(1, 7, 8))
+        processor(TinyH3Block(), torch.randn(1, 7, HIDDEN))
 
 
 def test_default_processor_loads_the_hip_kernel() -> None:
@@ -110,11 +133,21 @@ def test_forward_op_rejects_unsupported_semantics(kwargs) -> None:
 
 
 def test_forward_op_returns_lse_on_request() -> None:
-    def kernel(q, k, v, softmax_scale=None, causal=False):
-        return v, "lse"
+    # The kernel's LSE is (B, H, S); the forward op hands Diffusers'
+    # context-parallel template (B, S, H), a transposed view.
+    lse_bhs = torch.arange(2 * 3 * 5, dtype=torch.float32).reshape(2, 3, 5)
+    out = torch.zeros(2, 5, 3, 4)
 
-    assert hip_forward_op(None, 1, 2, 3, kernel=kernel) == 3
-    assert hip_forward_op(None, 1, 2, 3, return_lse=True, kernel=kernel) == (3, "lse")
+    def kernel(q, k, v, softmax_scale=None, causal=False):
+        return out, lse_bhs
+
+    assert hip_forward_op(None, 1, 2, 3, kernel=kernel) is out
+    o, lse = hip_forward_op(None, 1, 2, 3, return_lse=True, kernel=kernel)
+    assert o is out
+    assert lse.shape == (2, 5, 3)
+    assert torch.equal(lse, lse_bhs.permute(0, 2, 1))
+    assert lse.data_ptr() == lse_bhs.data_ptr()  # a view, no copy
+    assert (out + lse.unsqueeze(-1)).shape == out.shape  # the template's broadcast
 
 
 def test_kernel_callable_rejects_causal_and_host_tensors() -> None:
@@ -142,7 +175,7 @@ class FakeTransformer(torch.nn.Module):
     def __init__(self, n: int) -> None:
         super().__init__()
 
-        class MiniMaxH3Attention(Attention):
+        class MiniMaxH3Attention(TinyH3Block):
             def set_processor(self, processor):
                 self.processor = processor
 

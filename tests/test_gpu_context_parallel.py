@@ -96,7 +96,9 @@ def test_ring_schedule_on_one_device(chunks):
 
 def test_forward_op_with_lse_feeds_the_merge():
     """The context-parallel template's per-chunk calls: hip_forward_op with
-    return_lse on BHSD... here BSHD chunks of one sequence, then the merge."""
+    return_lse on BSHD chunks of one sequence gives (B, S, H) LSEs, which
+    broadcast against the output as the template's ring merge uses them, and
+    which merge_attention takes with lse_layout='bsh'."""
 
     g = torch.Generator().manual_seed(5)
     q, k, v = (torch.randn((2, 777, 3, 128), generator=g).to(torch.bfloat16).to(DEV) for _ in range(3))
@@ -104,13 +106,34 @@ def test_forward_op_with_lse_feeds_the_merge():
         hip_forward_op(None, q, k[:, a:b], v[:, a:b], return_lse=True, scale=0.1)
         for a, b in ((0, 300), (300, 301), (301, 777))
     ]
-    o, l = merge_attention([p[0] for p in parts], [p[1] for p in parts])
+    for o_i, l_i in parts:
+        assert l_i.shape == (2, 777, 3) and o_i.shape == (2, 777, 3, 128)
+    o, l = merge_attention([p[0] for p in parts], [p[1] for p in parts], lse_layout="bsh")
+    assert l.shape == (2, 777, 3)
     full_o, full_l = flash_attn_func(q, k, v, softmax_scale=0.1)
     ro, rl = sdpa_reference(q.cpu(), k.cpu(), v.cpu(), scale=0.1)
     m = error_metrics(o.float().cpu(), ro)
     assert m["max_abs"] <= ATTN_MAX_ABS and m["mean_abs"] <= ATTN_MEAN_ABS, m
-    assert (l.cpu() - rl).abs().max().item() <= LSE_MAX_ABS
-    assert (l - full_l).abs().max().item() <= LSE_MAX_ABS
+    assert (l.transpose(1, 2).cpu() - rl).abs().max().item() <= LSE_MAX_ABS
+    assert (l.transpose(1, 2) - full_l).abs().max().item() <= LSE_MAX_ABS
+
+    # The template's own two-part ring update on (B, S, H, 1) LSEs
+    # (out = prev - sigmoid(lse - prev_lse) * (prev - out)) over the same
+    # chunks equals the merge.
+    prev_o, prev_l = None, None
+    for o_i, l_i in parts:
+        o_i, l_i = o_i.float(), l_i.unsqueeze(-1)
+        if prev_o is not None:
+            o_i = prev_o - torch.sigmoid(l_i - prev_l) * (prev_o - o_i)
+            l_i = prev_l - torch.nn.functional.logsigmoid(prev_l - l_i)
+        prev_o, prev_l = o_i, l_i
+    assert (prev_o - o.float()).abs().max().item() <= 2e-2
+    assert (prev_l.squeeze(-1) - l).abs().max().item() <= 1e-5
+
+    # A caller's contiguous (B, S, H) LSE buffer is filled in place.
+    buf = torch.empty((2, 777, 3), device=DEV)
+    _, l2 = merge_attention([p[0] for p in parts], [p[1] for p in parts], lse=buf, lse_layout="bsh")
+    assert l2 is buf and torch.equal(buf, l)
 
 
 def test_merge_errors():
@@ -126,3 +149,7 @@ def test_merge_errors():
         merge_attention([o, o], [l, l], out=torch.empty((1, 4, 2, 128), dtype=torch.bfloat16))
     with pytest.raises(ValueError, match="lse must be"):
         merge_attention([o, o], [l, l], lse=torch.empty((1, 2, 4)))
+    with pytest.raises(ValueError, match="'bsh' LSEs"):
+        merge_attention([o, o], [l, l], lse_layout="bsh")  # (B, H, S) given as (B, S, H)
+    with pytest.raises(ValueError, match="lse_layout"):
+        merge_attention([o], [l], lse_layout="hbs")
