@@ -38,6 +38,7 @@
 #include "common.h"
 #include "kernels.h"
 
+
 namespace h3a {
 namespace {
 
@@ -56,6 +57,12 @@ constexpr float kSumLimit = 65536.0f;            // row-sum bound of the fast so
 // p of 2^127 * (2 - 2^-8) or more is finite in fp32 but rounds to inf in bf16,
 // and a rescale by 2^-ex with ex > 126 is subnormal; below 2^64 neither occurs.
 constexpr float kRecomputeLimit = 0x1p64f;
+// Rows a K / V buffer resource spans from its base: the main loop rebases
+// both at the first tile of every group of four iterations and loads up to
+// five tiles past the group's last one (tiles j .. j+8 from base j), so
+// 32-bit buffer offsets only ever cover one window of the view, however long
+// the view is.
+constexpr int kWindowRows = kBN * 9;
 constexpr int kQueuePieces = 4;                  // key-range pieces per tile of a dynamic tail
 constexpr int kQueueMinKeyTiles = 16;            // fewest key tiles in such a piece
 
@@ -95,6 +102,12 @@ __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory
 // One query tile (piece < 0) or one key-range piece of a split tile. All
 // waves of the workgroup call it with the same arguments; it returns with
 // no LDS DMA in flight.
+// kWide: views whose span reaches 2^31 bytes. Their K / V buffer resources
+// are rebased every four key tiles (a window of kWindowRows rows), so 32-bit
+// offsets never cover more than one window. Shorter views keep one resource
+// per view: the rebase needs scalar registers this kernel does not have to
+// spare (the compiler spills them), so it is not paid where it is not needed.
+template <bool kWide>
 __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int piece) {
     __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
     // V stages 0..3 first, then K stages 0..3: with a per-lane base in a VGPR
@@ -138,17 +151,39 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
         sk = min(sk - kt0 * kBN, (kt1 - kt0) * kBN);
     }
 
-    const char* qb = (const char*)p.q + 2 * (b * p.q_sb + h * p.q_sh) + (int64_t)q0 * p.q_rs;
+    // The Q resource starts at the tile's first query row; K / V resources
+    // start at the first key row of their window (kWide) or of the view.
+    const int q_first = kWide ? m0 : 0;  // first row of the Q resource, from the segment's
+    const char* qb = (const char*)p.q + 2 * (b * p.q_sb + h * p.q_sh) + (int64_t)(q0 + q_first) * p.q_rs;
     const char* kb = (const char*)p.k + 2 * (b * p.k_sb + h * p.k_sh) + (int64_t)k0 * p.k_rs;
     const char* vb = (const char*)p.v + 2 * (b * p.v_sb + h * p.v_sh) + (int64_t)k0 * p.v_rs;
+    // The window of a K / V view starting at key tile j0 (kWide), or the
+    // whole view: rows past the view's end are outside the range and load as
+    // zeros.
+    auto window = [&](const char* base, int row_bytes, int j0) {
+        if constexpr (kWide)
+            return make_rsrc_words(base + (int64_t)j0 * (kBN * row_bytes),
+                                   span_bytes(min(sk - j0 * kBN, kWindowRows), row_bytes));
+        else
+            return make_rsrc_words(base, span_bytes(sk, row_bytes));
+    };
     // The Q loads and the K / V DMA are written as inline asm, so the
     // compiler tracks none of them: it cannot tell the LDS stages apart and
     // would otherwise wait for every DMA in flight (vmcnt(0)) before the
     // first LDS read that follows one. Their completion is ordered explicitly
     // with wait_vmcnt, barriers and register pins below.
-    const i32x4 rq = make_rsrc_words(qb, span_bytes(sq, p.q_rs));
-    const i32x4 rk = make_rsrc_words(kb, span_bytes(sk, p.k_rs));
-    const i32x4 rv = make_rsrc_words(vb, span_bytes(sk, p.v_rs));
+    const i32x4 rq = make_rsrc_words(qb, span_bytes(kWide ? min(sq - m0, kBM) : sq, p.q_rs));
+    i32x4 rk = window(kb, p.k_rs, 0);
+    i32x4 rv = window(vb, p.v_rs, 0);
+    // Moves a window (kWide) four key tiles on, to start at tile j0: the
+    // 48-bit base of words 0-1 (stride bits zero) grows by 4 * kBN rows; the
+    // range is recomputed from the rows left.
+    auto advance = [&](i32x4& r, int row_bytes, int j0) {
+        const uint64_t base = ((uint64_t)(uint32_t)r.y << 32 | (uint32_t)r.x) + (uint64_t)(4 * kBN) * (uint32_t)row_bytes;
+        r.x = (int)(uint32_t)base;
+        r.y = (int)((uint32_t)(base >> 32) & 0xffffu);
+        r.z = (int)span_bytes(min(sk - j0 * kBN, kWindowRows), row_bytes);
+    };
 
     // Q fragment: lane holds query row (m0 + 32*wave + l32), head dims
     // 16*ks + 8*hi .. +8 for ks = 0..7 (B operand of S^T = K Q^T).
@@ -159,7 +194,7 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
         i32x4 raw;
         asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen"
                      : "=v"(raw)
-                     : "v"((uint32_t)(mq * p.q_rs + ks * 32 + hi * 16)), "s"(rq)
+                     : "v"((uint32_t)((mq - q_first) * p.q_rs + ks * 32 + hi * 16)), "s"(rq)
                      : "memory");
         qf[ks] = __builtin_bit_cast(bf16x8, raw);
     }
@@ -180,7 +215,7 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
     // buffer_load ... lds writes 16 bytes per lane to LDS address M0 + 16*lane;
     // M0 needs one wait state before the load reads it. Nothing else in this
     // kernel uses M0 (it is a reserved register, so it is not listed as
-    // clobbered).
+    // clobbered). `tile` counts from the current window's first tile.
     auto dma1 = [&](const i32x4& rsrc, int row_bytes, const uint32_t* lanes, char* stage, int tile, int i) {
         const uint32_t skip = (uint32_t)(tile * kBN * row_bytes);
         const uint32_t dst = (uint32_t)(uintptr_t)(const lds_char*)(stage + (wave * kDmaPerTile + i) * 4 * kRow);
@@ -271,11 +306,16 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
     // above it, and O and l rescaled to that offset. Leaves every p <= 1.
     const auto rk_plain = make_rsrc(kb, span_bytes(sk, p.k_rs));
     auto overflow = [&](int tile, bf16x8* pout, float& lsum) __attribute__((always_inline)) {
+        // K rows of the tile, from a resource at the tile's first row (kWide)
+        // or at the view's.
+        const int first = kWide ? tile * kBN : 0;
+        const auto rk_tile =
+            kWide ? make_rsrc(kb + (int64_t)first * p.k_rs, span_bytes(min(sk - first, kBN), p.k_rs)) : rk_plain;
         f32x16 s2[2] = {f32x16{}, f32x16{}};
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
-            const uint32_t row = (uint32_t)(tile * kBN + 32 * (t & 1) + l32);
-            const i32x4 raw = buf_load16(rk_plain, row * (uint32_t)p.k_rs + (t >> 1) * 32 + hi * 16);
+            const uint32_t row = (uint32_t)(tile * kBN - first + 32 * (t & 1) + l32);
+            const i32x4 raw = buf_load16(rk_tile, row * (uint32_t)p.k_rs + (t >> 1) * 32 + hi * 16);
             s2[t & 1] =
                 __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, raw), qf[t >> 1], s2[t & 1], 0, 0, 0);
         }
@@ -492,13 +532,25 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
     }
     auto step = [&](auto u, int jj) __attribute__((always_inline)) {
         constexpr int U = decltype(u)::value;
+        // A group of four iterations starts at tile jj: rebase the K / V
+        // windows there. Its iterations load K up to tile jj+8 and V up to
+        // jj+6, inside the window's kWindowRows.
+        if constexpr (kWide && U == 0) {
+            if (jj > 0) {
+                advance(rk, p.k_rs, jj);
+                advance(rv, p.v_rs, jj);
+            }
+        }
+        // Tile numbers of the DMA: counted from the window's first tile, jj - U
+        // (kWide), or from the view's first tile.
+        const int jt = kWide ? U : jj;
         // The four loads are spread over the iteration so that their LDS
         // writes do not arrive as one burst that holds up the fragment reads.
         auto hook = [&](int k) __attribute__((always_inline)) {
-            if (k == 0) dma_k1(jj + 5, (U + 1) & 3, 0);
-            if (k == 8) dma_k1(jj + 5, (U + 1) & 3, 1);
-            if (k == 16) dma_v1(jj + 3, (U + 3) & 3, 0);
-            if (k == 24) dma_v1(jj + 3, (U + 3) & 3, 1);
+            if (k == 0) dma_k1(jt + 5, (U + 1) & 3, 0);
+            if (k == 8) dma_k1(jt + 5, (U + 1) & 3, 1);
+            if (k == 16) dma_v1(jt + 3, (U + 3) & 3, 0);
+            if (k == 24) dma_v1(jt + 3, (U + 3) & 3, 1);
         };
         if constexpr (U & 1)
             iterate(std::true_type{}, kSoftmax, std::true_type{}, (U + 2) & 3, U, jj + 1, sa, sb, pfb, pfa,
@@ -559,6 +611,7 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
 // that the workgroups after the whole tiles take from a counter in the
 // workspace as they free up, so CUs that ran their whole tiles faster (XCD
 // clocks differ) take more of the tail.
+template <bool kWide>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     __shared__ int queue_head;
     // Workgroups are dispatched round-robin over the 8 XCDs, workgroup i to
@@ -598,7 +651,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // code (a single call inside the loop below changed its register
     // allocation and made it 1-2% slower).
     if (!queued) {
-        attn_tile(p, tile, piece);
+        attn_tile<kWide>(p, tile, piece);
         return;
     }
     for (;;) {
@@ -607,7 +660,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         piece = __builtin_amdgcn_readfirstlane(queue_head);  // uniform: keep it scalar
         __syncthreads();  // every wave has read queue_head before it is written again
         if ((unsigned)piece >= (unsigned)(p.split_n * p.split_tiles)) return;
-        attn_tile(p, p.n_full + piece % p.split_tiles, piece);
+        attn_tile<kWide>(p, p.n_full + piece % p.split_tiles, piece);
     }
 }
 
@@ -688,9 +741,10 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
 
 int attn_fwd_block_m() { return kBM; }
 int attn_fwd_block_n() { return kBN; }
+int attn_fwd_window_rows() { return kWindowRows > kBM ? kWindowRows : kBM; }
 int attn_fwd_row_margin() { return kBM + kBN * (2 * kStages + 2); }
 
-SplitPlan plan_attn_split(int64_t tiles, int64_t key_tiles, int cus) {
+SplitPlan plan_attn_split(int64_t tiles, int64_t key_tiles, int cus, int64_t max_workspace) {
     SplitPlan plan{(int32_t)tiles, 0, 0, 0, 0, 0};
     if (cus < 8 || cus % 8 != 0 || tiles <= 0) return plan;
     const int64_t piece_bytes = (int64_t)kBM * (kD + 1) * (int64_t)sizeof(float);
@@ -699,17 +753,19 @@ SplitPlan plan_attn_split(int64_t tiles, int64_t key_tiles, int cus) {
         // last round's tiles become kQueuePieces key-range pieces each, taken
         // from a counter by cus workgroups (at most) as CUs free up. Pieces
         // keep at least kQueueMinKeyTiles key tiles, so the pipeline's fill
-        // and drain stay small against a piece.
-        int n = kQueuePieces;
-        while (n > 1 && key_tiles / n < kQueueMinKeyTiles) --n;
-        if (n < 2) return plan;
+        // and drain stay small against a piece; fewer pieces are cut when
+        // their partial results would not fit in max_workspace.
         const int64_t full = (tiles - 1) / cus * cus, rest = tiles - full;
+        auto bytes = [&](int n) { return ((int64_t)n * rest * piece_bytes + 255) / 256 * 256 + 256; };
+        int n = kQueuePieces;
+        while (n > 1 && (key_tiles / n < kQueueMinKeyTiles || bytes(n) > max_workspace)) --n;
+        if (n < 2) return plan;
         plan.n_full = (int32_t)full;
         plan.split_n = n;
         plan.split_tiles = (int32_t)rest;
         plan.queue_blocks = (int32_t)(rest * n < cus ? rest * n : cus);
         plan.queue_offset = ((int64_t)n * rest * piece_bytes + 255) / 256 * 256;
-        plan.workspace_bytes = plan.queue_offset + 256;
+        plan.workspace_bytes = bytes(n);
         return plan;
     }
     // One partial round: its tiles are cut into n key-range pieces when that
@@ -722,6 +778,7 @@ SplitPlan plan_attn_split(int64_t tiles, int64_t key_tiles, int cus) {
     double best = 1.0;
     int best_n = 0;
     for (int n = 2; n <= 8 && n <= key_tiles; ++n) {
+        if ((int64_t)n * tiles * piece_bytes > max_workspace) break;
         const double cost = (double)((tiles * n + cus - 1) / cus) / n;
         if (cost < best - 0.05) {
             best = cost;
@@ -746,7 +803,10 @@ hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
     } else if (p.split_n != 0) {
         blocks = (int64_t)p.n_full + (int64_t)p.split_n * p.split_tiles;
     }
-    hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, p);
+    if (p.wide)
+        hipLaunchKernelGGL(attn_fwd_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, stream, p);
+    else
+        hipLaunchKernelGGL(attn_fwd_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.split_n == 0) return e;
     const dim3 merge_grid((unsigned)(p.split_tiles * (kBM / kMergeRows)));

@@ -23,7 +23,7 @@ int fail(int code, const char* fmt, ...) {
     return code;
 }
 
-constexpr int64_t kMaxSpan = (int64_t)1 << 31;  // buffer offsets are 32-bit
+constexpr int64_t kMaxWindow = (int64_t)1 << 31;  // buffer offsets are 32-bit
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
@@ -62,7 +62,6 @@ int prepare_attn(const h3a_attn_args* a, h3a::AttnParams& p, bool* empty) {
     }
 
     const bool varlen = a->cu_seqlens_q != nullptr;
-    int64_t rows_q = a->seqlen_q, rows_k = a->seqlen_k;
     p.q = a->q; p.k = a->k; p.v = a->v; p.o = a->o; p.lse = a->lse;
     p.q_sb = a->q_stride[0]; p.q_sh = a->q_stride[2];
     p.k_sb = a->k_stride[0]; p.k_sh = a->k_stride[2];
@@ -95,15 +94,23 @@ int prepare_attn(const h3a_attn_args* a, h3a::AttnParams& p, bool* empty) {
         p.seqlen_q = (int32_t)a->seqlen_q;
         p.seqlen_k = (int32_t)a->seqlen_k;
     }
-    // Every (batch, head) view is addressed with 32-bit byte offsets that may
-    // run a few tiles past the last row.
-    const int64_t rows[4] = {rows_q, rows_k, rows_k, rows_q};
-    const int64_t margin = h3a::attn_fwd_row_margin();
+    // The kernel addresses a view through buffer resources rebased to each
+    // query tile and each window of key tiles, with 32-bit byte offsets
+    // inside them: a view may be of any length, but attn_fwd_window_rows()
+    // rows of it must span less than 2^31 bytes.
+    const int64_t window = h3a::attn_fwd_window_rows();
     for (int i = 0; i < 4; ++i) {
-        const int64_t span = (rows[i] + margin) * st[i][1] * 2;
-        if (span >= kMaxSpan)
-            return fail(H3A_EUNSUPPORTED, "h3a_attn_fwd: %s view spans %lld bytes (limit 2^31)", nm[i], (long long)span);
+        const int64_t span = window * st[i][1] * 2;
+        if (span >= kMaxWindow)
+            return fail(H3A_EUNSUPPORTED, "h3a_attn_fwd: %s row stride %lld elements is too large (%lld rows must span < 2^31 bytes)",
+                        nm[i], (long long)st[i][1], (long long)window);
     }
+    // Views short enough for one buffer resource each (rows plus the
+    // kernel's margin under 2^31 bytes) take the narrow form.
+    const int64_t rows[4] = {a->seqlen_q, a->seqlen_k, a->seqlen_k, a->seqlen_q};
+    p.wide = 0;
+    for (int i = 0; i < 4; ++i)
+        if ((rows[i] + h3a::attn_fwd_row_margin()) * st[i][1] * 2 >= kMaxWindow) p.wide = 1;
     p.q_rs = (int32_t)(a->q_stride[1] * 2);
     p.k_rs = (int32_t)(a->k_stride[1] * 2);
     p.v_rs = (int32_t)(a->v_stride[1] * 2);
@@ -130,12 +137,25 @@ int device_cus() {
 
 // Split plan of a validated launch: dense inputs only (varlen tiles are not
 // uniform work).
-h3a::SplitPlan attn_plan(const h3a_attn_args* a, const h3a::AttnParams& p) {
+h3a::SplitPlan attn_plan(const h3a_attn_args* a, const h3a::AttnParams& p, int64_t max_workspace = INT64_MAX) {
     const int64_t tiles = (int64_t)p.n_qtiles * p.heads * p.n_groups;
     h3a::SplitPlan none{(int32_t)tiles, 0, 0, 0, 0, 0};
     if (a->cu_seqlens_q != nullptr) return none;
     const int bn = h3a::attn_fwd_block_n();
-    return h3a::plan_attn_split(tiles, (a->seqlen_k + bn - 1) / bn, device_cus());
+    return h3a::plan_attn_split(tiles, (a->seqlen_k + bn - 1) / bn, device_cus(), max_workspace);
+}
+
+// Points the launch at a workspace for the plan's split tiles.
+void apply_plan(h3a::AttnParams& p, const h3a::SplitPlan& plan, void* workspace) {
+    p.n_full = plan.n_full;
+    p.split_n = plan.split_n;
+    p.split_tiles = plan.split_tiles;
+    p.ws_o = (float*)workspace;
+    p.ws_lse = p.ws_o + (int64_t)plan.split_n * plan.split_tiles * h3a::attn_fwd_block_m() * 128;
+    if (plan.queue_blocks > 0) {
+        p.queue = (int*)((char*)workspace + plan.queue_offset);
+        p.queue_blocks = plan.queue_blocks;
+    }
 }
 
 // Shared checks of the modulation entry points. Fills the table, index and
@@ -200,21 +220,14 @@ int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
     if (rc != H3A_OK || empty) return rc;
     const h3a::SplitPlan plan = attn_plan(a, p);
     if (plan.split_n != 0 && a->workspace != nullptr && a->workspace_bytes >= plan.workspace_bytes &&
-        ((uintptr_t)a->workspace & 255u) == 0) {
-        p.n_full = plan.n_full;
-        p.split_n = plan.split_n;
-        p.split_tiles = plan.split_tiles;
-        p.ws_o = (float*)a->workspace;
-        p.ws_lse = p.ws_o + (int64_t)plan.split_n * plan.split_tiles * h3a::attn_fwd_block_m() * 128;
-        if (plan.queue_blocks > 0) {
-            p.queue = (int*)((char*)a->workspace + plan.queue_offset);
-            p.queue_blocks = plan.queue_blocks;
-        }
-    }
+        ((uintptr_t)a->workspace & 255u) == 0)
+        apply_plan(p, plan, a->workspace);
     hipError_t e = h3a::launch_attn_fwd(p, (hipStream_t)stream);
     if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_attn_fwd: launch failed: %s", hipGetErrorString(e));
     return H3A_OK;
 }
+
+
 
 int64_t h3a_attn_fwd_workspace_size(const h3a_attn_args* a) {
     g_err[0] = '\0';

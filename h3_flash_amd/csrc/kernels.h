@@ -42,6 +42,9 @@ struct AttnParams {
     // the pieces run out. NULL: pieces are assigned statically.
     int* queue;
     int32_t queue_blocks;
+    // Some view spans 2^31 bytes or more: K / V buffer resources are rebased
+    // per window of key tiles.
+    int32_t wide;
 };
 
 // How the query tiles of a dense launch are spread over the CUs.
@@ -51,12 +54,17 @@ struct SplitPlan {
     int64_t queue_offset;   // byte offset of the tail counter in the workspace
     int64_t workspace_bytes;
 };
-SplitPlan plan_attn_split(int64_t tiles, int64_t key_tiles, int cus);
+// max_workspace bounds the plan's workspace_bytes (fewer pieces, or none).
+SplitPlan plan_attn_split(int64_t tiles, int64_t key_tiles, int cus, int64_t max_workspace);
 
 int attn_fwd_block_m();
 int attn_fwd_block_n();
-// Rows past the end of a sequence that the kernel may address (all reads there
-// are bounds-checked buffer loads returning zero).
+// Rows one buffer resource of the kernel spans from its base (a query tile, or
+// a window of key tiles in the wide form); their bytes must stay below 2^31.
+int attn_fwd_window_rows();
+// Rows past the end of a view that the narrow form may address (all reads
+// there are bounds-checked buffer loads returning zero): a view whose rows
+// plus this margin span less than 2^31 bytes takes the narrow form.
 int attn_fwd_row_margin();
 hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream);
 

@@ -88,7 +88,7 @@ def _attn_args(**overrides):
         ({"cu_seqlens_q": 1 << 20, "num_segments": 1, "max_seqlen_q": 8}, _ext.H3A_EINVAL, "cu_seqlens_k"),
         ({"cu_seqlens_q": 1 << 20, "cu_seqlens_k": 1 << 20, "num_segments": 1, "max_seqlen_q": 99},
          _ext.H3A_EINVAL, "max_seqlen_q"),
-        ({"seqlen_q": 1 << 23, "seqlen_k": 1 << 23}, _ext.H3A_EUNSUPPORTED, "2^31"),
+        ({"q_stride": (ctypes.c_int64 * 3)(1 << 25, 1 << 21, 128)}, _ext.H3A_EUNSUPPORTED, "row stride"),
         ({"lse": (1 << 20) + 2}, _ext.H3A_EINVAL, "lse must be 4-byte aligned"),
         ({"lse": 1 << 20, "lse_stride": (ctypes.c_int64 * 2)(-16, 16)}, _ext.H3A_EINVAL, "non-negative strides"),
     ],

@@ -1,0 +1,81 @@
+"""GPU parity of attention on views that span 2 GiB or more.
+
+The reference's seam hands the kernel ``to_qkv(...).chunk(3)`` views of any
+length (src/h3_flash/runtime/attention/dense_fa4.py:123-131,145). Views whose
+rows span 2^31 bytes or more take the kernel's wide form, whose K / V buffer
+resources are rebased per window of key tiles. The narrow form runs the same
+tiles in the same order on a contiguous copy, so both must give the same
+bits; sampled rows are also checked against the CPU oracle.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from h3_flash_amd import flash_attn_func
+from oracle.attention import sdpa_rows
+from oracle.metrics import ATTN_MAX_ABS, ATTN_MEAN_ABS, LSE_MAX_ABS, error_metrics
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def _check_rows(q, k, v, out, lse, rows, cu=None, tag=""):
+    ref_o, ref_l = sdpa_rows(q.cpu(), k.cpu(), v.cpu(), rows, cu_seqlens=cu)
+    idx = rows.to(DEV)
+    m = error_metrics(out[:, idx].float().cpu(), ref_o)
+    lse_err = (lse[:, :, idx].cpu().double() - ref_l.double()).abs().max().item()
+    assert m["finite"] and m["max_abs"] <= ATTN_MAX_ABS and m["mean_abs"] <= ATTN_MEAN_ABS, (tag, m)
+    assert lse_err <= LSE_MAX_ABS, (tag, lse_err)
+
+
+def test_fused_projection_views_of_40_heads_past_2gib():
+    """to_qkv output chunked into q/k/v views at 40 heads and S = 72,003: each
+    view spans 72,003 rows x 30,720 bytes = 2.21 GB (dynamic tail, ragged
+    last query and key tiles)."""
+
+    S, H, D = 72_003, 40, 128
+    print(f"case: to_qkv views S={S} H={H}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(41)
+    qkv = torch.randn((1, S, 3 * H * D), device=DEV, generator=g).to(torch.bfloat16)
+    q, k, v = (t.unflatten(-1, (H, D)) for t in qkv.chunk(3, dim=-1))
+    assert q.stride(1) * 2 * S >= 2**31
+    out, lse = flash_attn_func(q, k, v)
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    del qkv
+    out_c, lse_c = flash_attn_func(qc, kc, vc)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_c) and torch.equal(lse, lse_c)
+    rows = torch.tensor([0, 1, 255, 256, 40_000, S - 258, S - 3, S - 2, S - 1])
+    _check_rows(qc, kc, vc, out, lse, rows, tag="to_qkv views")
+
+
+def test_views_past_4gib_dense_split_and_varlen():
+    """One head each of q, k and v as column slices of a (40,000, 65,536)
+    buffer: 128 KiB rows, a 5.24 GB span (offsets past 2^32 bytes). The dense
+    launch has 157 tiles on the chip (key-range split); the varlen launch has
+    a segment starting at key row 17,001."""
+
+    S, W, D = 40_000, 1 << 16, 128
+    print(f"case: column views S={S} row stride {W}", flush=True)
+    buf = torch.empty((1, S, 1, W), dtype=torch.bfloat16, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(43)
+    buf[..., : 3 * D] = torch.randn((1, S, 1, 3 * D), device=DEV, generator=g).to(torch.bfloat16)
+    q, k, v = buf[..., :D], buf[..., D : 2 * D], buf[..., 2 * D : 3 * D]
+    assert q.stride(1) * 2 * S >= 2**32
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+
+    out, lse = flash_attn_func(q, k, v)
+    out_c, lse_c = flash_attn_func(qc, kc, vc)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_c) and torch.equal(lse, lse_c)
+    _check_rows(qc, kc, vc, out, lse, torch.tensor([0, 17_000, 33_333, S - 1]), tag="dense")
+
+    cu = torch.tensor([0, 17_001, S], dtype=torch.int32, device=DEV)
+    kw = {"cu_seqlens_q": cu, "cu_seqlens_k": cu, "max_seqlen_q": S - 17_001}
+    out, lse = flash_attn_func(q, k, v, **kw)
+    out_c, lse_c = flash_attn_func(qc, kc, vc, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_c) and torch.equal(lse, lse_c)
+    _check_rows(qc, kc, vc, out, lse, torch.tensor([0, 17_000, 17_001, 30_000, S - 1]), cu=cu.cpu(), tag="varlen")
