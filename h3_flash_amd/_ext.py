@@ -26,6 +26,9 @@ H3A_DTYPE_F32 = 1
 H3A_DTYPE_I32 = 2
 H3A_DTYPE_I64 = 3
 
+# Bytes of the device array behind h3a_attn_fwd_noalloc (H3A_NOALLOC_SCRATCH_BYTES).
+H3A_NOALLOC_SCRATCH_BYTES = 64 << 20
+
 _I64x3 = ctypes.c_int64 * 3
 _I64x2 = ctypes.c_int64 * 2
 
@@ -238,6 +241,7 @@ class AttnMergeArgs(ctypes.Structure):
 SIGNATURES = {
     "h3a_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
     "h3a_attn_fwd_workspace_size": (ctypes.c_int64, [ctypes.POINTER(AttnArgs)]),
+    "h3a_attn_fwd_noalloc": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
     "h3a_qknorm_rope": (ctypes.c_int, [ctypes.POINTER(QkNormRopeArgs), ctypes.c_void_p]),
     "h3a_pack_qkv": (ctypes.c_int, [ctypes.POINTER(PackQkvArgs), ctypes.c_void_p]),
     "h3a_merge_heads": (ctypes.c_int, [ctypes.POINTER(MergeHeadsArgs), ctypes.c_void_p]),

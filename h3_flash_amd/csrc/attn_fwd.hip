@@ -33,11 +33,19 @@
 // chunk c ^ swz(r), swz(r) = 4*(r & 3) + ((r >> 2) & 3). Both read patterns are
 // then bank-conflict free: the K reads (16 consecutive rows, one chunk) and the
 // V transpose reads (4 consecutive rows x 4 chunks per 32 lanes).
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
 #include "kernels.h"
 
+// Workspace of h3a_attn_fwd_noalloc: the fp32 partial results of the tail's
+// key-range pieces and the tail's counter, for callers that cannot allocate.
+// Every GPU the library runs on holds its own copy until the process ends.
+// Host code never passes `scratch` itself (on the host it names a shadow
+// variable, not device memory): attn_static_scratch looks up this device's
+// copy with hipGetSymbolAddress and kernels take that address.
+static __device__ __align__(256) char scratch[h3a::kStaticScratchBytes];
 
 namespace h3a {
 namespace {
@@ -791,6 +799,27 @@ SplitPlan plan_attn_split(int64_t tiles, int64_t key_tiles, int cus, int64_t max
     plan.split_tiles = (int32_t)tiles;
     plan.workspace_bytes = (int64_t)best_n * tiles * piece_bytes;
     return plan;
+}
+
+hipError_t attn_static_scratch(void** ptr) {
+    // Looked up once per device (with that device current), then cached.
+    static std::atomic<void*> cache[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev >= 0 && dev < 64) {
+        void* hit = cache[dev].load(std::memory_order_acquire);
+        if (hit != nullptr) {
+            *ptr = hit;
+            return hipSuccess;
+        }
+    }
+    void* addr = nullptr;
+    e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (dev >= 0 && dev < 64) cache[dev].store(addr, std::memory_order_release);
+    *ptr = addr;
+    return hipSuccess;
 }
 
 hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {

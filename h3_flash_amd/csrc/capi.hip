@@ -227,7 +227,28 @@ int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
     return H3A_OK;
 }
 
-
+int h3a_attn_fwd_noalloc(const h3a_attn_args* a, void* stream) {
+    g_err[0] = '\0';
+    h3a::AttnParams p{};
+    bool empty = false;
+    const int rc = prepare_attn(a, p, &empty);
+    if (rc != H3A_OK || empty) return rc;
+    void* scratch = nullptr;
+    hipError_t e = h3a::attn_static_scratch(&scratch);
+    if (e != hipSuccess)
+        return fail(H3A_ELAUNCH, "h3a_attn_fwd_noalloc: device scratch lookup failed: %s", hipGetErrorString(e));
+    // The plan is fitted to the scratch (fewer key-range pieces, or none), so
+    // this only rejects a plan that could not be fitted. No allocation, no
+    // memset: the tail's counter is zeroed by a kernel of the launch.
+    const h3a::SplitPlan plan = attn_plan(a, p, h3a::kStaticScratchBytes);
+    if (plan.workspace_bytes > h3a::kStaticScratchBytes)
+        return fail(H3A_EINVAL, "h3a_attn_fwd_noalloc: the launch needs %lld bytes of scratch, the static scratch holds %lld",
+                    (long long)plan.workspace_bytes, (long long)h3a::kStaticScratchBytes);
+    if (plan.split_n != 0) apply_plan(p, plan, scratch);
+    e = h3a::launch_attn_fwd(p, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_attn_fwd_noalloc: launch failed: %s", hipGetErrorString(e));
+    return H3A_OK;
+}
 
 int64_t h3a_attn_fwd_workspace_size(const h3a_attn_args* a) {
     g_err[0] = '\0';

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "h3attn.h"
+
 namespace h3a {
 
 // Validated attention launch description. Strides are in elements.
@@ -56,6 +58,12 @@ struct SplitPlan {
 };
 // max_workspace bounds the plan's workspace_bytes (fewer pieces, or none).
 SplitPlan plan_attn_split(int64_t tiles, int64_t key_tiles, int cus, int64_t max_workspace);
+
+// Bytes of the file-scope device array that serves as the workspace of the
+// allocation-free attention entry point, and the lookup of the current
+// device's copy (hipGetSymbolAddress, cached per device).
+constexpr int64_t kStaticScratchBytes = H3A_NOALLOC_SCRATCH_BYTES;
+hipError_t attn_static_scratch(void** ptr);
 
 int attn_fwd_block_m();
 int attn_fwd_block_n();

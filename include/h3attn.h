@@ -138,6 +138,28 @@ H3A_API int h3a_attn_fwd(const h3a_attn_args *args, void *stream);
 H3A_API int64_t h3a_attn_fwd_workspace_size(const h3a_attn_args *args);
 
 /*
+ * h3a_attn_fwd without allocation. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory per call (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).
+ *
+ * Same arguments, semantics and results (up to the rounding of the key-range
+ * pieces) as h3a_attn_fwd; `workspace` / `workspace_bytes` are ignored. The
+ * split tail's fp32 partial results and counter live in a file-scope device
+ * array of H3A_NOALLOC_SCRATCH_BYTES (64 MiB) that every GPU the library
+ * runs on holds until the process ends; its address is looked up once per
+ * device. The split plan is fitted to that array (fewer key-range pieces,
+ * or none), so any problem size runs; a plan that could not be fitted would
+ * be rejected with H3A_EINVAL. The call allocates nothing, issues no memset
+ * and does not synchronise.
+ *
+ * All calls on one GPU share its array: calls that overlap on one GPU (on
+ * different streams, or from different threads without ordering) race on
+ * it and give wrong results. Order them on one stream.
+ */
+#define H3A_NOALLOC_SCRATCH_BYTES ((int64_t)64 << 20)
+H3A_API int h3a_attn_fwd_noalloc(const h3a_attn_args *args, void *stream);
+
+/*
  * Fused per-head RMSNorm + rotate-half RoPE on q and k in one launch:
  *   r      = rsqrt(mean(x^2) + eps)            (over head_dim, fp32)
  *   n[c]   = x[c] * r * w[c]

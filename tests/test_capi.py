@@ -35,6 +35,7 @@ def test_header_declares_the_expected_entry_points():
     assert declared_functions() == [
         "h3a_abi_version",
         "h3a_attn_fwd",
+        "h3a_attn_fwd_noalloc",
         "h3a_attn_fwd_workspace_size",
         "h3a_attn_merge",
         "h3a_last_error",
