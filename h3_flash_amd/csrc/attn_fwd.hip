@@ -89,6 +89,15 @@ __device__ __forceinline__ uint32_t span_bytes(int rows, int row_bytes) {
 
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
+// LDS chunk swizzle of a d-major V tile (128-byte rows): 16 consecutive rows
+// read at one logical chunk hit 16 different 16-byte bank groups.
+__device__ __forceinline__ int vswz(int r) { return (r >> 1) & 7; }
+
+// Key order of the S^T rows with a d-major V: bits 2 and 3 of the row index
+// swapped. A lane then holds keys 8*hi .. 8*hi + 7 of every 16-key step of
+// P^T, which one ds_read_b128 of a d-major V row matches.
+__device__ __forceinline__ int keyperm(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
+
 // Four bf16 of one head-dim column: within each 16-lane group lane i receives
 // element (i & 3) of the 8-byte chunks addressed by lanes 4j + (i >> 2).
 __device__ __forceinline__ i32x2 read_tr(const lds_char* p) {
@@ -115,7 +124,12 @@ __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory
 // offsets never cover more than one window. Shorter views keep one resource
 // per view: the rebase needs scalar registers this kernel does not have to
 // spare (the compiler spills them), so it is not paid where it is not needed.
-template <bool kWide>
+// kVT: V is read from a d-major copy (p.vt: per (batch, head) 128 rows of
+// keys, zero past the last key), so each PV fragment is one ds_read_b128
+// instead of two transpose reads. The K rows of every 16-key group are then
+// taken in the order that swaps bits 2 and 3 of the key index (keyperm), so
+// that the eight keys a lane holds in P^T are consecutive.
+template <bool kWide, bool kVT>
 __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int piece) {
     __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
     // V stages 0..3 first, then K stages 0..3: with a per-lane base in a VGPR
@@ -133,6 +147,8 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int hi = lane >> 5;  // wave half
     const int l32 = lane & 31;
+    // Key (within a 32-key block) of S^T row r.
+    auto krowperm = [](int r) { return kVT ? keyperm(r) : r; };
 
     const int qt = tile % p.n_qtiles;
     const int rest = tile / p.n_qtiles;
@@ -164,7 +180,10 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
     const int q_first = kWide ? m0 : 0;  // first row of the Q resource, from the segment's
     const char* qb = (const char*)p.q + 2 * (b * p.q_sb + h * p.q_sh) + (int64_t)(q0 + q_first) * p.q_rs;
     const char* kb = (const char*)p.k + 2 * (b * p.k_sb + h * p.k_sh) + (int64_t)k0 * p.k_rs;
-    const char* vb = (const char*)p.v + 2 * (b * p.v_sb + h * p.v_sh) + (int64_t)k0 * p.v_rs;
+    // d-major V: key k0 of dim row 0 of this head; a head's block is 128 rows
+    // of vt_rs bytes.
+    const char* vb = kVT ? (const char*)p.vt + 2 * (b * p.vt_sb + h * p.vt_sh + (int64_t)k0)
+                         : (const char*)p.v + 2 * (b * p.v_sb + h * p.v_sh) + (int64_t)k0 * p.v_rs;
     // The window of a K / V view starting at key tile j0 (kWide), or the
     // whole view: rows past the view's end are outside the range and load as
     // zeros.
@@ -182,7 +201,10 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
     // with wait_vmcnt, barriers and register pins below.
     const i32x4 rq = make_rsrc_words(qb, span_bytes(kWide ? min(sq - m0, kBM) : sq, p.q_rs));
     i32x4 rk = window(kb, p.k_rs, 0);
-    i32x4 rv = window(vb, p.v_rs, 0);
+    // The d-major V resource ends at the end of this head's block: tiles past
+    // the padded key range read the next dim row's keys (finite values that
+    // meet P = 0) or, in the last row, zeros.
+    i32x4 rv = kVT ? make_rsrc_words(vb, (uint32_t)(kD * p.vt_rs - 2 * k0)) : window(vb, p.v_rs, 0);
     // Moves a window (kWide) four key tiles on, to start at tile j0: the
     // 48-bit base of words 0-1 (stride bits zero) grows by 4 * kBN rows; the
     // range is recomputed from the rows left.
@@ -219,13 +241,22 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
         const int chunk = ((lane & 15) ^ swz(r)) << 4;
         dk[i] = (uint32_t)(r * p.k_rs + chunk);
         dv[i] = (uint32_t)(r * p.v_rs + chunk);
+        if constexpr (kVT) {
+            // d-major V tile: 128 rows (head dims) of 128 bytes (64 keys); lane
+            // L writes LDS chunk (L & 7) of row rt + (L >> 3), which holds the
+            // row's 16-byte chunk (L & 7) ^ vswz(row).
+            const int rt = (wave * kDmaPerTile + i) * 8 + (lane >> 3);
+            dv[i] = (uint32_t)(rt * p.vt_rs + (((lane & 7) ^ vswz(rt)) << 4));
+        }
     }
     // buffer_load ... lds writes 16 bytes per lane to LDS address M0 + 16*lane;
     // M0 needs one wait state before the load reads it. Nothing else in this
     // kernel uses M0 (it is a reserved register, so it is not listed as
     // clobbered). `tile` counts from the current window's first tile.
     auto dma1 = [&](const i32x4& rsrc, int row_bytes, const uint32_t* lanes, char* stage, int tile, int i) {
-        const uint32_t skip = (uint32_t)(tile * kBN * row_bytes);
+        // A tile is kBN rows of row_bytes, or (d-major V, row_bytes 0) 2 * kBN
+        // bytes along every dim row.
+        const uint32_t skip = (uint32_t)(tile * (row_bytes != 0 ? kBN * row_bytes : 2 * kBN));
         const uint32_t dst = (uint32_t)(uintptr_t)(const lds_char*)(stage + (wave * kDmaPerTile + i) * 4 * kRow);
         asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                      :
@@ -234,7 +265,7 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
     };
     // Load i (of kDmaPerTile) of this wave's share of a K / V tile.
     auto dma_k1 = [&](int tile, int stage, int i) { dma1(rk, p.k_rs, dk, kst + stage * kTile, tile, i); };
-    auto dma_v1 = [&](int tile, int stage, int i) { dma1(rv, p.v_rs, dv, vst + stage * kTile, tile, i); };
+    auto dma_v1 = [&](int tile, int stage, int i) { dma1(rv, kVT ? 0 : p.v_rs, dv, vst + stage * kTile, tile, i); };
     auto dma_k = [&](int tile, int stage) {
 #pragma unroll
         for (int i = 0; i < kDmaPerTile; ++i) dma_k1(tile, stage, i);
@@ -249,7 +280,8 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
     // The swizzle only moves bits 4-7 of an in-row byte offset, so every
     // fragment address is a per-lane base XOR a per-step constant. K: offset
     // kbase ^ (32*ks) (+32 rows for the second key block).
-    const int kbase = l32 * kRow + ((hi ^ swz(l32)) << 4);
+    const int krow = kVT ? keyperm(l32) : l32;
+    const int kbase = krow * kRow + ((hi ^ swz(krow)) << 4);
     // Transpose-read addresses of PV MFMA t (head-dim block db = t >> 2, key
     // step cc = t & 3): lane (g = l & 15) of a 16-lane group reads row
     // 16*cc + 4*hi + (g >> 2) (+8 for the upper four keys) and head dims
@@ -278,31 +310,43 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
     // and of the V transpose reads (one per head-dim block and key half); the
     // empty asm keeps each in a register so stage and step offsets become
     // instruction immediates.
-    uint32_t kofs[8], vofs[8];
+    // d-major V (kVT): the A fragment of PV MFMA (db, cc) is row 32*db + l32,
+    // logical chunk 2*cc + hi, stored at chunk (2*cc + hi) ^ vswz(l32): a
+    // per-lane base XOR 32*cc, plus 4096*db.
+    constexpr int kVofs = kVT ? 4 : 8;
+    uint32_t kofs[8], vofs[kVofs];
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) {
         kofs[ks] = (uint32_t)(kStages * kTile + (kbase ^ (32 * ks)));
         asm volatile("" : "+v"(kofs[ks]));
     }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        vofs[i] = (uint32_t)(vbase ^ (64 * (i >> 1)) ^ (32 * (i & 1)));
+    for (int i = 0; i < kVofs; ++i) {
+        if constexpr (kVT)
+            vofs[i] = (uint32_t)((l32 * 2 * kBN + ((hi ^ vswz(l32)) << 4)) ^ (32 * i));
+        else
+            vofs[i] = (uint32_t)(vbase ^ (64 * (i >> 1)) ^ (32 * (i & 1)));
         asm volatile("" : "+v"(vofs[i]));
     }
     auto kread = [&](int stage, int t) {
         return *(const lds_bf16x8*)(lds + kofs[t >> 1] + (stage * kTile + (t & 1) * 32 * kRow));
     };
-    auto vread = [&](int stage, int t) {
-        const lds_char* a = lds + (stage * kTile + (t & 3) * 16 * kRow);
-        const i32x2 lo = read_tr(a + vofs[2 * (t >> 2)]);
-        const i32x2 up = read_tr(a + 8 * kRow + vofs[2 * (t >> 2) + 1]);
-        return __builtin_bit_cast(bf16x8, i32x4{lo.x, lo.y, up.x, up.y});
+    // A fragment of PV MFMA (head-dim block db, 16-key step cc).
+    auto vread = [&](int stage, int db, int cc) {
+        if constexpr (kVT) {
+            return *(const lds_bf16x8*)(lds + vofs[cc] + (stage * kTile + db * 32 * 2 * kBN));
+        } else {
+            const lds_char* a = lds + (stage * kTile + cc * 16 * kRow);
+            const i32x2 lo = read_tr(a + vofs[2 * db]);
+            const i32x2 up = read_tr(a + 8 * kRow + vofs[2 * db + 1]);
+            return __builtin_bit_cast(bf16x8, i32x4{lo.x, lo.y, up.x, up.y});
+        }
     };
     auto mask_tail = [&](f32x16& s0, f32x16& s1, int tile) {
         const int n0 = tile * kBN;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const int key = n0 + (r >> 2) * 8 + hi * 4 + (r & 3);
+            const int key = n0 + krowperm((r >> 2) * 8 + hi * 4 + (r & 3));
             if (key >= sk) s0[r] = -INFINITY;
             if (key + 32 >= sk) s1[r] = -INFINITY;
         }
@@ -322,7 +366,7 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
         f32x16 s2[2] = {f32x16{}, f32x16{}};
 #pragma unroll
         for (int t = 0; t < 16; ++t) {
-            const uint32_t row = (uint32_t)(tile * kBN - first + 32 * (t & 1) + l32);
+            const uint32_t row = (uint32_t)(tile * kBN - first + 32 * (t & 1) + krow);
             const i32x4 raw = buf_load16(rk_tile, row * (uint32_t)p.k_rs + (t >> 1) * 32 + hi * 16);
             s2[t & 1] =
                 __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, raw), qf[t >> 1], s2[t & 1], 0, 0, 0);
@@ -424,7 +468,7 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
             for (int t = 0; t < 16; ++t) {
                 s_out[t & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[t & 3], qf[t >> 1], s_out[t & 1], 0, 0, 0);
                 if (t + 4 < 16) kf[t & 3] = kread(kl, t + 4);
-                if (kPV && t >= 12) vf[t - 12] = vread(vl, t - 12);
+                if (kPV && t >= 12) vf[t - 12] = vread(vl, t - 12, 0);
                 hook(t);
                 slice(t);
                 __builtin_amdgcn_sched_barrier(0);
@@ -433,12 +477,12 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
         if constexpr (kPV) {
             if constexpr (!kQK) {
 #pragma unroll
-                for (int t = 0; t < 4; ++t) vf[t] = vread(vl, t);
+                for (int t = 0; t < 4; ++t) vf[t] = vread(vl, t, 0);
             }
 #pragma unroll
             for (int t = 0; t < 16; ++t) {
-                oacc[t >> 2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[t & 3], pin[t & 3], oacc[t >> 2], 0, 0, 0);
-                if (t + 4 < 16) vf[t & 3] = vread(vl, t + 4);
+                oacc[t & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf[t & 3], pin[t >> 2], oacc[t & 3], 0, 0, 0);
+                if (t + 4 < 16) vf[t & 3] = vread(vl, (t + 4) & 3, (t + 4) >> 2);
                 if (t >= 12 && kl_next >= 0) kf[t - 12] = kread(kl_next, t - 12);
                 hook((kQK ? 16 : 0) + t);
                 slice((kQK ? 16 : 0) + t);
@@ -546,19 +590,20 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
         if constexpr (kWide && U == 0) {
             if (jj > 0) {
                 advance(rk, p.k_rs, jj);
-                advance(rv, p.v_rs, jj);
+                if constexpr (!kVT) advance(rv, p.v_rs, jj);
             }
         }
         // Tile numbers of the DMA: counted from the window's first tile, jj - U
         // (kWide), or from the view's first tile.
         const int jt = kWide ? U : jj;
+        const int jv = kWide && !kVT ? U : jj;  // the d-major V resource is never rebased
         // The four loads are spread over the iteration so that their LDS
         // writes do not arrive as one burst that holds up the fragment reads.
         auto hook = [&](int k) __attribute__((always_inline)) {
             if (k == 0) dma_k1(jt + 5, (U + 1) & 3, 0);
             if (k == 8) dma_k1(jt + 5, (U + 1) & 3, 1);
-            if (k == 16) dma_v1(jt + 3, (U + 3) & 3, 0);
-            if (k == 24) dma_v1(jt + 3, (U + 3) & 3, 1);
+            if (k == 16) dma_v1(jv + 3, (U + 3) & 3, 0);
+            if (k == 24) dma_v1(jv + 3, (U + 3) & 3, 1);
         };
         if constexpr (U & 1)
             iterate(std::true_type{}, kSoftmax, std::true_type{}, (U + 2) & 3, U, jj + 1, sa, sb, pfb, pfa,
@@ -619,7 +664,7 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
 // that the workgroups after the whole tiles take from a counter in the
 // workspace as they free up, so CUs that ran their whole tiles faster (XCD
 // clocks differ) take more of the tail.
-template <bool kWide>
+template <bool kWide, bool kVT>
 __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     __shared__ int queue_head;
     // Workgroups are dispatched round-robin over the 8 XCDs, workgroup i to
@@ -659,7 +704,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // code (a single call inside the loop below changed its register
     // allocation and made it 1-2% slower).
     if (!queued) {
-        attn_tile<kWide>(p, tile, piece);
+        attn_tile<kWide, kVT>(p, tile, piece);
         return;
     }
     for (;;) {
@@ -668,7 +713,45 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         piece = __builtin_amdgcn_readfirstlane(queue_head);  // uniform: keep it scalar
         __syncthreads();  // every wave has read queue_head before it is written again
         if ((unsigned)piece >= (unsigned)(p.split_n * p.split_tiles)) return;
-        attn_tile<kWide>(p, p.n_full + piece % p.split_tiles, piece);
+        attn_tile<kWide, kVT>(p, p.n_full + piece % p.split_tiles, piece);
+    }
+}
+
+// d-major copy of V for the kVT form: vt holds, per (batch, head), 128 rows
+// (head dims) of vt_rs bytes with keys contiguous, zero from seqlen_k to the
+// next multiple of kBN. One workgroup moves a 64-key x 128-dim block through
+// LDS: 16-byte row loads in, 16-byte dim-row stores out (8 lanes per 128-byte
+// row). Rows are 65 dwords in LDS, so both phases are bank-conflict free.
+__global__ __launch_bounds__(256) void attn_vt_kernel(AttnParams p) {
+    __shared__ uint32_t blk[kBN * 65];
+    const int t = threadIdx.x;
+    const int k0 = blockIdx.x * kBN, h = blockIdx.y, b = blockIdx.z;
+    const char* src = (const char*)p.v + 2 * (b * p.v_sb + h * p.v_sh);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int key = i * 16 + (t >> 4), c = t & 15;
+        i32x4 x = i32x4{0, 0, 0, 0};
+        if (k0 + key < p.seqlen_k) x = *(const i32x4*)(src + (int64_t)(k0 + key) * p.v_rs + c * 16);
+        uint32_t* row = blk + key * 65 + c * 4;
+        row[0] = (uint32_t)x.x;
+        row[1] = (uint32_t)x.y;
+        row[2] = (uint32_t)x.z;
+        row[3] = (uint32_t)x.w;
+    }
+    __syncthreads();
+    char* dst = (char*)p.vt + 2 * (b * p.vt_sb + h * p.vt_sh + (int64_t)k0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int d = i * 32 + (t >> 3), kc = t & 7;
+        const int sh = (d & 1) * 16;
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t lo = blk[(8 * kc + 2 * j) * 65 + (d >> 1)] >> sh;
+            const uint32_t up = blk[(8 * kc + 2 * j + 1) * 65 + (d >> 1)] >> sh;
+            w[j] = (lo & 0xffffu) | (up << 16);
+        }
+        *(i32x4*)(dst + (int64_t)d * p.vt_rs + kc * 16) = i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
     }
 }
 
@@ -832,10 +915,19 @@ hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
     } else if (p.split_n != 0) {
         blocks = (int64_t)p.n_full + (int64_t)p.split_n * p.split_tiles;
     }
-    if (p.wide)
-        hipLaunchKernelGGL(attn_fwd_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, stream, p);
+    if (p.vt != nullptr) {
+        const dim3 tgrid((unsigned)((p.seqlen_k + kBN - 1) / kBN), (unsigned)p.heads, (unsigned)p.n_groups);
+        hipLaunchKernelGGL(attn_vt_kernel, tgrid, dim3(256), 0, stream, p);
+    }
+    const dim3 grid((unsigned)blocks), block(kThreads);
+    if (p.wide && p.vt != nullptr)
+        hipLaunchKernelGGL((attn_fwd_kernel<true, true>), grid, block, 0, stream, p);
+    else if (p.wide)
+        hipLaunchKernelGGL((attn_fwd_kernel<true, false>), grid, block, 0, stream, p);
+    else if (p.vt != nullptr)
+        hipLaunchKernelGGL((attn_fwd_kernel<false, true>), grid, block, 0, stream, p);
     else
-        hipLaunchKernelGGL(attn_fwd_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, stream, p);
+        hipLaunchKernelGGL((attn_fwd_kernel<false, false>), grid, block, 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.split_n == 0) return e;
     const dim3 merge_grid((unsigned)(p.split_tiles * (kBM / kMergeRows)));

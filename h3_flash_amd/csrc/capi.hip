@@ -145,6 +145,33 @@ h3a::SplitPlan attn_plan(const h3a_attn_args* a, const h3a::AttnParams& p, int64
     return h3a::plan_attn_split(tiles, (a->seqlen_k + bn - 1) / bn, device_cus(), max_workspace);
 }
 
+// The workspace of a launch: the split plan's partial results and counter,
+// then (dense launches, allow_vt) a d-major copy of V, 128 rows of keys per
+// (batch, head) padded to a multiple of 64 keys.
+struct AttnWorkspace {
+    h3a::SplitPlan plan;
+    int64_t vt_offset;  // 0: no d-major V
+    int64_t vt_rs;      // bytes per row of keys
+    int64_t total;
+};
+
+AttnWorkspace attn_workspace(const h3a_attn_args* a, const h3a::AttnParams& p, bool allow_vt,
+                             int64_t max_workspace = INT64_MAX) {
+    AttnWorkspace w{attn_plan(a, p, max_workspace), 0, 0, 0};
+    w.total = w.plan.workspace_bytes;
+    const int bn = h3a::attn_fwd_block_n();
+    const int64_t vt_rs = (a->seqlen_k + bn - 1) / bn * bn * 2;
+    // The d-major V is addressed with 32-bit offsets within a head's block.
+    if (!allow_vt || a->cu_seqlens_q != nullptr || a->seqlen_k == 0 || 128 * vt_rs >= kMaxWindow) return w;
+    const int64_t offset = (w.total + 255) / 256 * 256;
+    const int64_t bytes = a->batch * a->heads * 128 * vt_rs;
+    if (offset + bytes > max_workspace) return w;
+    w.vt_offset = offset;
+    w.vt_rs = vt_rs;
+    w.total = offset + bytes;
+    return w;
+}
+
 // Points the launch at a workspace for the plan's split tiles.
 void apply_plan(h3a::AttnParams& p, const h3a::SplitPlan& plan, void* workspace) {
     p.n_full = plan.n_full;
@@ -218,10 +245,16 @@ int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
     bool empty = false;
     const int rc = prepare_attn(a, p, &empty);
     if (rc != H3A_OK || empty) return rc;
-    const h3a::SplitPlan plan = attn_plan(a, p);
-    if (plan.split_n != 0 && a->workspace != nullptr && a->workspace_bytes >= plan.workspace_bytes &&
-        ((uintptr_t)a->workspace & 255u) == 0)
-        apply_plan(p, plan, a->workspace);
+    const AttnWorkspace w = attn_workspace(a, p, true);
+    if (w.total > 0 && a->workspace != nullptr && a->workspace_bytes >= w.total && ((uintptr_t)a->workspace & 255u) == 0) {
+        if (w.plan.split_n != 0) apply_plan(p, w.plan, a->workspace);
+        if (w.vt_rs != 0) {
+            p.vt = (char*)a->workspace + w.vt_offset;
+            p.vt_rs = (int32_t)w.vt_rs;
+            p.vt_sh = 128 * (w.vt_rs / 2);
+            p.vt_sb = a->heads * p.vt_sh;
+        }
+    }
     hipError_t e = h3a::launch_attn_fwd(p, (hipStream_t)stream);
     if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_attn_fwd: launch failed: %s", hipGetErrorString(e));
     return H3A_OK;
@@ -256,7 +289,7 @@ int64_t h3a_attn_fwd_workspace_size(const h3a_attn_args* a) {
     bool empty = false;
     const int rc = prepare_attn(a, p, &empty);
     if (rc != H3A_OK) return rc;
-    return empty ? 0 : attn_plan(a, p).workspace_bytes;
+    return empty ? 0 : attn_workspace(a, p, true).total;
 }
 
 int h3a_qknorm_rope(const h3a_qknorm_rope_args* a, void* stream) {

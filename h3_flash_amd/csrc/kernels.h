@@ -47,6 +47,12 @@ struct AttnParams {
     // Some view spans 2^31 bytes or more: K / V buffer resources are rebased
     // per window of key tiles.
     int32_t wide;
+    // d-major V (dense launches with a workspace; NULL: V is read as given):
+    // attn_vt_kernel writes, per (batch, head), 128 rows of vt_rs bytes with
+    // keys contiguous, zero past seqlen_k up to a multiple of 64 keys.
+    void* vt;
+    int64_t vt_sb, vt_sh;  // batch / head strides of vt, in elements
+    int32_t vt_rs;         // bytes per head-dim row, a multiple of 128
 };
 
 // How the query tiles of a dense launch are spread over the CUs.

@@ -90,16 +90,24 @@ extern "C" {
  *
  * Rows with no key (seqlen_k == 0) produce O = 0 and LSE = -inf.
  *
- * Workspace (dense inputs only): with more query tiles (256 rows of one
- * head) than the GPU has CUs, the tiles of the last round run as key-range
- * pieces that workgroups take from a counter in the workspace as CUs free
- * up; with fewer tiles, when they would keep less than 70% of the CUs busy
- * (B=1 H=4 S=4096: 64 tiles on 256 CUs), they run as statically assigned
- * pieces. Either way the fp32 partial results are merged by a second kernel
- * on the same stream (the counter is zeroed by a small kernel first). That needs h3a_attn_fwd_workspace_size(args) bytes of
- * device memory at `workspace` (256-byte aligned); with a NULL or smaller
- * workspace every tile runs whole. The results differ only by rounding.
- * Calls sharing one workspace must be ordered (same stream).
+ * Workspace (dense inputs only), h3a_attn_fwd_workspace_size(args) bytes of
+ * device memory at `workspace` (256-byte aligned, contents on entry
+ * irrelevant), used for two things:
+ *   - the split tail: with more query tiles (256 rows of one head) than the
+ *     GPU has CUs, the tiles of the last round run as key-range pieces that
+ *     workgroups take from a counter in the workspace as CUs free up; with
+ *     fewer tiles, when they would keep less than 70% of the CUs busy (B=1
+ *     H=4 S=4096: 64 tiles on 256 CUs), they run as statically assigned
+ *     pieces. Either way the fp32 partial results are merged by a second
+ *     kernel on the same stream (the counter is zeroed by a small kernel
+ *     first);
+ *   - a d-major copy of V (per batch and head, 128 rows of keys padded with
+ *     zeros to a multiple of 64), written by a transpose kernel at the start
+ *     of the call, from which the attention kernel reads each PV fragment
+ *     with one 16-byte LDS read.
+ * With a NULL or smaller workspace every tile runs whole on V as given. The
+ * results differ only by rounding. Calls sharing one workspace must be
+ * ordered (same stream).
  */
 typedef struct h3a_attn_args {
     int32_t abi_version; /* must be H3A_ABI_VERSION */
