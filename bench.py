@@ -47,6 +47,7 @@ def parse_args(argv=None):
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-relayout", action="store_true", help="skip the relayout, row-fusion and context-parallel merge rates")
     p.add_argument("--no-block", action="store_true", help="skip the whole-attention-block timing")
+    p.add_argument("--no-sdpa", action="store_true", help="skip torch's GPU SDPA and the numerical comparison with it")
     p.add_argument(
         "--copy-calibration",
         type=int,
@@ -343,7 +344,8 @@ def block_rates(torch, heads: int = 40, head_dim: int = 128, grid=(32, 30, 52)) 
 
 
 def read_pmc_traffic() -> dict | None:
-    """HBM bytes per attention launch from the committed rocprofv3 PMC summary."""
+    """HBM bytes per attention call from the committed rocprofv3 PMC summary,
+    with the sha256 of the library those counters were collected with."""
 
     if not PMC_SUMMARY.is_file():
         return None
@@ -354,7 +356,105 @@ def read_pmc_traffic() -> dict | None:
         if m is None:
             return None
         out[key] = float(m.group(1))
+    m = re.search(r"^library_sha256:\s*([0-9a-f]{64})", text, flags=re.M)
+    out["library_sha256"] = m.group(1) if m else None
     return out
+
+
+def traffic_entry(traffic: dict | None, loaded_sha: str) -> tuple[float | None, dict]:
+    """``roofline.traffic`` and where it came from. The bytes are quoted only
+    when the committed counters were collected with the library this run
+    loaded; otherwise they would describe another kernel, and are null."""
+
+    source = {
+        "profile": str(PMC_SUMMARY.relative_to(ROOT)),
+        "profile_library_sha256": None if traffic is None else traffic["library_sha256"],
+        "loaded_library_sha256": loaded_sha,
+    }
+    match = traffic is not None and traffic["library_sha256"] == loaded_sha
+    source["match"] = match
+    if not match:
+        return None, source
+    return traffic["hbm_read_bytes_per_launch"] + traffic["hbm_write_bytes_per_launch"], source
+
+
+def reference_harness(torch, q, k, v, out, segments, hip_ms: float, flops: float, reps: int = 10) -> dict:
+    """The side-by-side report of benchmarks/benchmark_dense_fa4.py:84-136 on
+    the bench inputs: torch's GPU SDPA (BHSD transposes of the BSHD tensors,
+    its flash / memory-efficient backends; one call per packed segment) timed
+    on the same device, and the numerical block of the HIP output against it
+    (delta = sdpa - hip; relative L2 and cosine against the SDPA output)."""
+
+    from torch.nn import functional
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    bounds = [0]
+    for n in segments:
+        bounds.append(bounds[-1] + n)
+
+    def sdpa():
+        parts = []
+        for a, b in zip(bounds[:-1], bounds[1:]):
+            o = functional.scaled_dot_product_attention(
+                q[:, a:b].transpose(1, 2), k[:, a:b].transpose(1, 2), v[:, a:b].transpose(1, 2),
+                dropout_p=0.0, is_causal=False,
+            )
+            parts.append(o.transpose(1, 2))
+        return parts[0] if len(parts) == 1 else torch.cat(parts, dim=1)
+
+    try:
+        with torch.no_grad(), sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            native = sdpa()
+            torch.cuda.synchronize()
+            ms = _time_ms(torch, sdpa, reps=reps)
+    except RuntimeError as exc:  # no fused SDPA backend for this shape on this build
+        return {"torch_sdpa": None, "error": str(exc)[:200]}
+    ref = native.float()
+    delta = ref - out.float()
+    numerical = {
+        "torch_equal": bool(torch.equal(native, out)),
+        "finite": bool(torch.isfinite(out).all().item()),
+        "max_abs": delta.abs().max().item(),
+        "mean_abs": delta.abs().mean().item(),
+        "relative_l2": (delta.norm() / ref.norm().clamp_min(1e-12)).item(),
+        "cosine_similarity": torch.nn.functional.cosine_similarity(ref.flatten(), out.float().flatten(), dim=0).item(),
+    }
+    del native, ref, delta
+    return {
+        "torch_sdpa": {
+            "call": "F.scaled_dot_product_attention(q.transpose(1,2), k.transpose(1,2), v.transpose(1,2)) per segment, "
+            "flash / memory-efficient backends, torch " + torch.__version__,
+            "ms": ms,
+            "TFLOP_s": flops / (ms * 1e-3) / 1e12,
+        },
+        "hip_ms": hip_ms,
+        "median_speedup": ms / hip_ms,
+        "numerical": numerical,
+    }
+
+
+def workspace_bytes(q, k, v, out, lse, kw) -> int:
+    """Workspace bytes flash_attn_func asks the caching allocator for in
+    this call (split-tail partial results and the d-major V copy)."""
+
+    import ctypes
+
+    from h3_flash_amd import _ext
+    from h3_flash_amd.attention import _strides3
+
+    a = _ext.AttnArgs()
+    a.abi_version = _ext.ABI_VERSION
+    a.q, a.k, a.v, a.o, a.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
+    B, S, H, D = q.shape
+    a.batch, a.heads, a.seqlen_q, a.seqlen_k, a.head_dim = B, H, S, k.shape[1], D
+    a.q_stride[:], a.k_stride[:], a.v_stride[:], a.o_stride[:] = (_strides3(t) for t in (q, k, v, out))
+    a.lse_stride[:] = (lse.stride(0), lse.stride(1))
+    a.softmax_scale = D**-0.5
+    if kw:
+        a.cu_seqlens_q = a.cu_seqlens_k = kw["cu_seqlens_q"].data_ptr()
+        a.num_segments = kw["cu_seqlens_q"].numel() - 1
+        a.max_seqlen_q = kw["max_seqlen_q"]
+    return int(_ext.load_library().h3a_attn_fwd_workspace_size(ctypes.byref(a)))
 
 
 def main(argv=None) -> int:
@@ -415,6 +515,7 @@ def main(argv=None) -> int:
     def step():
         flash_attn_func(q, k, v, out=out, lse=lse, **kw)
 
+    torch.cuda.reset_peak_memory_stats(dev)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -437,10 +538,14 @@ def main(argv=None) -> int:
     ms_per_step = region_ms / args.steps
     kernel_ms = statistics.fmean(launch_ms)
 
+    peak_memory = torch.cuda.max_memory_allocated(dev)
     flops = w.flops
     value = flops / (ms_per_step * 1e-3) / 1e12
     achieved = flops / (kernel_ms * 1e-3) / 1e12
-    traffic = read_pmc_traffic()
+    from h3_flash_amd import _ext
+
+    loaded_sha = _ext.provenance()["sha256"]
+    traffic, traffic_source = traffic_entry(read_pmc_traffic(), loaded_sha)
     compulsory = 2 * (2 * w.seqlen * w.heads * w.head_dim * 2) + w.seqlen * w.heads * 4
 
     result = {
@@ -476,23 +581,27 @@ def main(argv=None) -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / PEAK_BF16_TFLOPS,
-            "traffic": (traffic["hbm_read_bytes_per_launch"] + traffic["hbm_write_bytes_per_launch"])
-            if traffic
-            else None,
+            "traffic": traffic,
+            "traffic_source": traffic_source,
             "kernel": "attn_fwd_kernel",
             # events around each call: for dense launches with more tiles than
-            # CUs that is attn_queue_reset + attn_fwd_kernel + attn_merge_kernel
-            # (the tail's pieces), all of them part of the attention
-            "kernel_ms_scope": "whole flash_attn_func call on its stream",
+            # CUs that is attn_vt_kernel (d-major V copy; it also zeroes the
+            # tail's counter) + attn_fwd_kernel + attn_merge_kernel (the tail's
+            # pieces), all of them part of the attention
+            "kernel_ms_scope": "whole flash_attn_func call on its stream: attn_vt_kernel (d-major V copy), "
+            "attn_fwd_kernel, attn_merge_kernel (the tail's pieces)",
             "kernel_ms_mean": kernel_ms,
             "kernel_ms_min": min(launch_ms),
             "algorithmic_flop_per_launch": flops,
             "compulsory_hbm_bytes_per_launch": compulsory,
         },
         "prologue": prologue,
+        "peak_gpu_memory_bytes": peak_memory,
+        "workspace_bytes": workspace_bytes(q, k, v, out, lse, kw),
         "wall_s_timed_region": wall,
         "device": torch.cuda.get_device_name(0),
     }
+    result["reference_harness"] = None if args.no_sdpa else reference_harness(torch, q, k, v, out, w.segments, ms_per_step, flops)
     result["relayout"] = None if args.no_relayout else relayout_rates(torch)
     result["fusions"] = None if args.no_relayout else fusion_rates(torch)
     result["cp_merge"] = None if args.no_relayout else merge_rates(torch)

@@ -726,6 +726,9 @@ __global__ __launch_bounds__(256) void attn_vt_kernel(AttnParams p) {
     __shared__ uint32_t blk[kBN * 65];
     const int t = threadIdx.x;
     const int k0 = blockIdx.x * kBN, h = blockIdx.y, b = blockIdx.z;
+    // The dynamic tail's counter, for the attention kernel that follows on
+    // the stream (instead of a launch of attn_queue_reset).
+    if (p.queue != nullptr && t == 0 && blockIdx.x == 0 && h == 0 && b == 0) *p.queue = 0;
     const char* src = (const char*)p.v + 2 * (b * p.v_sb + h * p.v_sh);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -910,7 +913,8 @@ hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
     if (tiles <= 0) return hipSuccess;
     int64_t blocks = tiles;
     if (p.queue != nullptr) {
-        hipLaunchKernelGGL(attn_queue_reset, dim3(1), dim3(64), 0, stream, p.queue);
+        // With a d-major V copy the transpose kernel zeroes the counter.
+        if (p.vt == nullptr) hipLaunchKernelGGL(attn_queue_reset, dim3(1), dim3(64), 0, stream, p.queue);
         blocks = (int64_t)p.n_full + p.queue_blocks;
     } else if (p.split_n != 0) {
         blocks = (int64_t)p.n_full + (int64_t)p.split_n * p.split_tiles;
