@@ -98,6 +98,13 @@ __device__ __forceinline__ int vswz(int r) { return (r >> 1) & 7; }
 // P^T, which one ds_read_b128 of a d-major V row matches.
 __device__ __forceinline__ int keyperm(int r) { return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1); }
 
+// First key of packed segment s (its first key row k0, clamped) in the
+// d-major V of a varlen launch: k0 rounded up to a multiple of 64, plus 64
+// per earlier segment. Segments never overlap there when the offsets ascend,
+// and every segment stays inside the rows of roundup(seqlen_k, 64) +
+// 64 * num_segments keys whatever the offsets hold.
+__device__ __forceinline__ int vt_segment_start(int k0, int s) { return (k0 + kBN - 1) / kBN * kBN + kBN * s; }
+
 // Four bf16 of one head-dim column: within each 16-lane group lane i receives
 // element (i & 3) of the 8-byte chunks addressed by lanes 4j + (i >> 2).
 __device__ __forceinline__ i32x2 read_tr(const lds_char* p) {
@@ -116,9 +123,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 // DMA loads in flight are waited for explicitly (wait_vmcnt) before it.
 __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
-// One query tile (piece < 0) or one key-range piece of a split tile. All
-// waves of the workgroup call it with the same arguments; it returns with
-// no LDS DMA in flight.
+// One query tile (chunk < 0), or key-range piece `chunk` of `chunks` of a
+// tile. A piece with a workspace slot (slot >= 0) writes normalised fp32
+// partial O and LSE there for the merge; a whole tile, or a piece covering
+// the tile's whole key range (slot < 0), writes O and LSE. All waves of the
+// workgroup call it with the same arguments; it returns with no LDS DMA in
+// flight.
 // kWide: views whose span reaches 2^31 bytes. Their K / V buffer resources
 // are rebased every four key tiles (a window of kWindowRows rows), so 32-bit
 // offsets never cover more than one window. Shorter views keep one resource
@@ -130,7 +140,7 @@ __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory
 // taken in the order that swaps bits 2 and 3 of the key index (keyperm), so
 // that the eight keys a lane holds in P^T are consecutive.
 template <bool kWide, bool kVT>
-__device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int piece) {
+__device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int chunk, int chunks, int slot) {
     __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
     // V stages 0..3 first, then K stages 0..3: with a per-lane base in a VGPR
     // every fragment read offset then fits the 16-bit ds_read immediate.
@@ -156,6 +166,7 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
     const int grp = rest / p.heads;
 
     int b = grp, q0 = 0, k0 = 0, sq = p.seqlen_q, sk = p.seqlen_k;
+    int vpad = 0;  // key offset of this segment in the d-major V
     if (p.cu_q != nullptr) {
         // Segment bounds are clamped to the packed rows, so no cu_seqlens
         // content can move an access outside the tensors.
@@ -164,13 +175,14 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
         sq = min(max(p.cu_q[grp + 1], q0), p.seqlen_q) - q0;
         k0 = min(max(p.cu_k[grp], 0), p.seqlen_k);
         sk = min(max(p.cu_k[grp + 1], k0), p.seqlen_k) - k0;
+        if (kVT) vpad = vt_segment_start(k0, grp) - k0;
     }
     const int m0 = qt * kBM;
     if (m0 >= sq) return;  // whole workgroup: tile beyond this segment
-    if (piece >= 0) {
-        // Piece c of split_n covers key tiles [c*n/split_n, (c+1)*n/split_n).
-        const int chunk = piece / p.split_tiles, nkt = (sk + kBN - 1) / kBN;
-        const int kt0 = chunk * nkt / p.split_n, kt1 = (chunk + 1) * nkt / p.split_n;
+    if (chunk >= 0) {
+        // Piece c of n covers key tiles [c*nkt/n, (c+1)*nkt/n).
+        const int nkt = (sk + kBN - 1) / kBN;
+        const int kt0 = chunk * nkt / chunks, kt1 = (chunk + 1) * nkt / chunks;
         k0 += kt0 * kBN;
         sk = min(sk - kt0 * kBN, (kt1 - kt0) * kBN);
     }
@@ -182,7 +194,7 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
     const char* kb = (const char*)p.k + 2 * (b * p.k_sb + h * p.k_sh) + (int64_t)k0 * p.k_rs;
     // d-major V: key k0 of dim row 0 of this head; a head's block is 128 rows
     // of vt_rs bytes.
-    const char* vb = kVT ? (const char*)p.vt + 2 * (b * p.vt_sb + h * p.vt_sh + (int64_t)k0)
+    const char* vb = kVT ? (const char*)p.vt + 2 * (b * p.vt_sb + h * p.vt_sh + (int64_t)(k0 + vpad))
                          : (const char*)p.v + 2 * (b * p.v_sb + h * p.v_sh) + (int64_t)k0 * p.v_rs;
     // The window of a K / V view starting at key tile j0 (kWide), or the
     // whole view: rows past the view's end are outside the range and load as
@@ -204,7 +216,7 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
     // The d-major V resource ends at the end of this head's block: tiles past
     // the padded key range read the next dim row's keys (finite values that
     // meet P = 0) or, in the last row, zeros.
-    i32x4 rv = kVT ? make_rsrc_words(vb, (uint32_t)(kD * p.vt_rs - 2 * k0)) : window(vb, p.v_rs, 0);
+    i32x4 rv = kVT ? make_rsrc_words(vb, (uint32_t)(kD * p.vt_rs - 2 * (k0 + vpad))) : window(vb, p.v_rs, 0);
     // Moves a window (kWide) four key tiles on, to start at tile j0: the
     // 48-bit base of words 0-1 (stride bits zero) grows by 4 * kBN rows; the
     // range is recomputed from the rows left.
@@ -629,10 +641,10 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
     }
     const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
     const float lse = l_run > 0.f ? (mc + __log2f(l_run)) * 0.69314718055994531f : -INFINITY;
-    if (piece >= 0) {
+    if (slot >= 0) {
         // Partial result of a key-range piece: normalised O and LSE in fp32.
         const int row = wave * 32 + l32;
-        float* wo = p.ws_o + ((int64_t)piece * kBM + row) * kD;
+        float* wo = p.ws_o + ((int64_t)slot * kBM + row) * kD;
 #pragma unroll
         for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -641,7 +653,7 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int pie
                 *(f32x4*)(wo + d) = f32x4{oacc[db][i * 4 + 0] * inv, oacc[db][i * 4 + 1] * inv,
                                           oacc[db][i * 4 + 2] * inv, oacc[db][i * 4 + 3] * inv};
             }
-        if (hi == 0) p.ws_lse[(int64_t)piece * kBM + row] = lse;
+        if (hi == 0) p.ws_lse[(int64_t)slot * kBM + row] = lse;
         return;
     }
     if (mq < sq) {
@@ -675,17 +687,25 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // B=1 H=5 S=49,920; 1.70 GB in dispatch order, at the same speed). A
     // static split (fewer tiles than CUs, n_full == 0) gives every workgroup
     // one piece, each XCD a contiguous range of them.
-    // Packed varlen grids keep dispatch order (tile i is workgroup i): their
-    // tiles past a short segment's end exit at once, and in dispatch order
-    // they spread over all XCDs. Contiguous ranges gave a few XCDs nearly
-    // only empty tiles (the 49,920 + 1,296 two-segment batch ran at half
-    // speed).
+    // Packed varlen launches with a work list (vplan) run the list's whole
+    // rounds the same way, XCD-contiguous over list positions, and take the
+    // last round's pieces from a counter. Without a list they keep dispatch
+    // order (tile i is workgroup i): tiles past a short segment's end exit at
+    // once, and in dispatch order they spread over all XCDs (contiguous
+    // ranges gave a few XCDs nearly only empty tiles: the 49,920 + 1,296
+    // two-segment batch ran at half speed).
     const int bid = blockIdx.x;
-    int tile = bid, piece = -1;
-    // With a tail queue, workgroups [n_full, grid) take the pieces of the
-    // last round's tiles from a counter, one at a time.
-    const bool queued = p.queue != nullptr && bid >= p.n_full;
-    if (p.cu_q == nullptr && !queued) {
+    int tile = bid, chunk = -1, chunks = 1, slot = -1;
+    const bool planned = p.vplan != nullptr;
+    // With a tail queue, the workgroups after the whole tiles take the pieces
+    // of the last round's tiles from a counter, one at a time.
+    const bool queued = planned ? bid >= p.ub_tiles : p.queue != nullptr && bid >= p.n_full;
+    if (planned && !queued) {
+        const int n_full = p.vplan[kPlanFull];
+        if (bid >= n_full) return;
+        const int pos = (n_full & 7) == 0 ? (bid & 7) * (n_full >> 3) + (bid >> 3) : bid;
+        tile = __builtin_amdgcn_readfirstlane(p.vlist[pos]);  // uniform: the addressing is scalar
+    } else if (p.cu_q == nullptr && !queued) {
         const int nb = p.queue != nullptr ? p.n_full : (int)gridDim.x;
         const int xcd = bid & 7, local = bid >> 3, per = nb >> 3, rem = nb & 7;
         const int start = xcd * per + min(xcd, rem);  // first tile of this XCD's share
@@ -695,8 +715,10 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
             if (local < full_per) {
                 tile = xcd * full_per + local;
             } else {
-                piece = start - xcd * full_per + (local - full_per);
-                tile = p.n_full + piece % p.split_tiles;
+                slot = start - xcd * full_per + (local - full_per);
+                tile = p.n_full + slot % p.split_tiles;
+                chunk = slot / p.split_tiles;
+                chunks = p.split_n;
             }
         }
     }
@@ -704,16 +726,165 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // code (a single call inside the loop below changed its register
     // allocation and made it 1-2% slower).
     if (!queued) {
-        attn_tile<kWide, kVT>(p, tile, piece);
+        attn_tile<kWide, kVT>(p, tile, chunk, chunks, slot);
         return;
     }
+    int* const counter = planned ? (int*)p.vplan + kPlanQueue : p.queue;
     for (;;) {
-        if (threadIdx.x == 0) queue_head = atomicAdd(p.queue, 1);
+        if (threadIdx.x == 0) queue_head = atomicAdd(counter, 1);
         __syncthreads();  // also: every wave is done with the previous piece's LDS
-        piece = __builtin_amdgcn_readfirstlane(queue_head);  // uniform: keep it scalar
+        const int piece = __builtin_amdgcn_readfirstlane(queue_head);  // uniform: keep it scalar
         __syncthreads();  // every wave has read queue_head before it is written again
-        if ((unsigned)piece >= (unsigned)(p.split_n * p.split_tiles)) return;
-        attn_tile<kWide, kVT>(p, p.n_full + piece % p.split_tiles, piece);
+        if (planned) {
+            if (piece >= p.vplan[kPlanPieces]) return;
+            // pieces[i] = (list position, chunk | chunks << 2 | (merge slot + 1) << 5)
+            const int pos = __builtin_amdgcn_readfirstlane(p.vpieces[2 * piece]);
+            const int code = __builtin_amdgcn_readfirstlane(p.vpieces[2 * piece + 1]);
+            const int merge_slot = (code >> 5) - 1;
+            tile = __builtin_amdgcn_readfirstlane(p.vlist[pos]);
+            chunk = code & 3;
+            chunks = (code >> 2) & 7;
+            slot = merge_slot >= 0 ? merge_slot * kQueuePieces + chunk : -1;
+        } else {
+            if ((unsigned)piece >= (unsigned)(p.split_n * p.split_tiles)) return;
+            tile = p.n_full + piece % p.split_tiles;
+            chunk = piece / p.split_tiles;
+            chunks = p.split_n;
+            slot = piece;
+        }
+        attn_tile<kWide, kVT>(p, tile, chunk, chunks, slot);
+    }
+}
+
+// The work list of a packed varlen launch, built on the device from the
+// segment offsets (the host does not have them) by one 256-thread workgroup:
+//   1. the query and key length of every segment (clamped as attn_tile
+//      clamps them);
+//   2. segments ordered by key length, longest first (ties: segment order;
+//      up to kPlanSortMax segments, beyond that in segment order), so the
+//      longest tiles run first and the last round holds the shortest;
+//   3. the non-empty (segment, head, query tile) tiles in that order, the
+//      heads and query tiles of one segment consecutive (they share K/V);
+//   4. n_full = the whole rounds but the last (as for dense launches), and
+//      the last round's tiles cut into key-range pieces (kQueuePieces, fewer
+//      when a piece would hold under kQueueMinKeyTiles key tiles; one piece
+//      writes the output itself), with merge slots for the split tiles;
+//   5. the counts, and the tail counter zeroed.
+constexpr int kPlanSortMax = 2048;
+
+// Exclusive prefix sum over the 256 threads; *total receives the sum.
+__device__ __forceinline__ int block_scan(int v, int* buf, int* total) {
+    const int t = threadIdx.x;
+    buf[t] = v;
+    __syncthreads();
+    for (int off = 1; off < 256; off <<= 1) {
+        const int add = t >= off ? buf[t - off] : 0;
+        __syncthreads();
+        buf[t] += add;
+        __syncthreads();
+    }
+    const int incl = buf[t];
+    *total = buf[255];
+    __syncthreads();
+    return incl - v;
+}
+
+__global__ __launch_bounds__(256) void attn_varlen_plan_kernel(AttnParams p) {
+    __shared__ int scan[256];
+    __shared__ int lk_s[kPlanSortMax];
+    const int t = threadIdx.x;
+    const int nseg = p.n_groups, heads = p.heads, nq = p.n_qtiles, cus = p.plan_cus;
+    int* const info = p.vplan_w;
+    int* const list = p.vlist_w;
+    int* const pieces = p.vpieces_w;
+    int* const merge = p.vmerge_w;
+    int* const segq = p.vscratch;
+    int* const segk = segq + nseg;
+    int* const order = segk + nseg;
+    int* const base = order + nseg;
+    const bool sorted = nseg <= kPlanSortMax;
+    for (int i = t; i < nseg; i += 256) {
+        const int q0 = min(max(p.cu_q[i], 0), p.seqlen_q);
+        const int k0 = min(max(p.cu_k[i], 0), p.seqlen_k);
+        segq[i] = min(max(p.cu_q[i + 1], q0), p.seqlen_q) - q0;
+        const int lk = min(max(p.cu_k[i + 1], k0), p.seqlen_k) - k0;
+        segk[i] = lk;
+        if (sorted) lk_s[i] = lk;
+    }
+    __syncthreads();
+    for (int i = t; i < nseg; i += 256) {
+        int r = i;
+        if (sorted) {
+            const int li = lk_s[i];
+            r = 0;
+            for (int j = 0; j < nseg; ++j) r += (lk_s[j] > li) | ((lk_s[j] == li) & (j < i));
+        }
+        order[r] = i;
+    }
+    __syncthreads();
+    // Tiles of the segments in that order (query rows past n_qtiles tiles
+    // are not computed: max_seqlen_q bounds every segment).
+    int carry = 0;
+    for (int c0 = 0; c0 < nseg; c0 += 256) {
+        const int r = c0 + t;
+        const int cnt = r < nseg ? min((segq[order[r]] + kBM - 1) / kBM, nq) * heads : 0;
+        int tot;
+        const int off = block_scan(cnt, scan, &tot);
+        if (r < nseg) base[r] = carry + off;
+        carry += tot;
+    }
+    // Offsets that ascend give at most ub_tiles tiles; others are cut there.
+    const int n_tiles = min(carry, p.ub_tiles);
+    __syncthreads();
+    for (int r = 0; r < nseg; ++r) {
+        const int seg = order[r];
+        const int tq = min((segq[seg] + kBM - 1) / kBM, nq);
+        const int b0 = base[r];
+        for (int u = t; u < tq * heads && b0 + u < n_tiles; u += 256) list[b0 + u] = (seg * heads + u / tq) * nq + u % tq;
+    }
+    const int n_full = n_tiles > cus ? (n_tiles - 1) / cus * cus : 0;
+    const int n_last = n_tiles - n_full;
+    int piece_carry = 0, merge_carry = 0;
+    for (int c0 = 0; c0 < n_last; c0 += 256) {
+        const int i = c0 + t;
+        int n = 0;
+        if (i < n_last) {
+            // Segment of list position n_full + i: the last r with base[r] <=
+            // the position (empty segments share their successor's base).
+            const int pos = n_full + i;
+            int lo = 0, hi = nseg - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (base[mid] <= pos) lo = mid; else hi = mid - 1;
+            }
+            const int nkt = (segk[order[lo]] + kBN - 1) / kBN;
+            n = kQueuePieces;
+            while (n > 1 && nkt / n < kQueueMinKeyTiles) --n;
+        }
+        int ptot, mtot;
+        const int poff = block_scan(n, scan, &ptot);
+        const int moff = block_scan(n > 1 ? 1 : 0, scan, &mtot);
+        if (i < n_last) {
+            const int pos = n_full + i;
+            const int ms = n > 1 ? merge_carry + moff : -1;
+            for (int c = 0; c < n; ++c) {
+                pieces[2 * (piece_carry + poff + c)] = pos;
+                pieces[2 * (piece_carry + poff + c) + 1] = c | (n << 2) | ((ms + 1) << 5);
+            }
+            if (ms >= 0) {
+                merge[2 * ms] = pos;
+                merge[2 * ms + 1] = n;
+            }
+        }
+        piece_carry += ptot;
+        merge_carry += mtot;
+    }
+    if (t == 0) {
+        info[kPlanTiles] = n_tiles;
+        info[kPlanFull] = n_full;
+        info[kPlanPieces] = piece_carry;
+        info[kPlanMerges] = merge_carry;
+        info[kPlanQueue] = 0;
     }
 }
 
@@ -725,16 +896,37 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
 __global__ __launch_bounds__(256) void attn_vt_kernel(AttnParams p) {
     __shared__ uint32_t blk[kBN * 65];
     const int t = threadIdx.x;
-    const int k0 = blockIdx.x * kBN, h = blockIdx.y, b = blockIdx.z;
+    const int h = blockIdx.y, b = blockIdx.z;
     // The dynamic tail's counter, for the attention kernel that follows on
     // the stream (instead of a launch of attn_queue_reset).
     if (p.queue != nullptr && t == 0 && blockIdx.x == 0 && h == 0 && b == 0) *p.queue = 0;
+    // Block x moves keys [64x, 64x + 64) of the d-major layout. Dense: key k
+    // of the sequence sits at k. Packed varlen: segment s starts at
+    // vt_segment_start (its own rows, padded to a multiple of 64).
+    const int k0 = blockIdx.x * kBN;
+    int src0 = k0, src_end = p.seqlen_k;
+    if (p.cu_k != nullptr) {
+        // The grid covers every key of the rows; keys outside every segment
+        // (padding, gaps) are written as zeros, so the attention kernel never
+        // reads uninitialised memory past a segment's end.
+        const int nseg = p.n_groups;
+        int lo = 0, hi = nseg - 1;  // the last segment starting at or before k0
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (vt_segment_start(min(max(p.cu_k[mid], 0), p.seqlen_k), mid) <= k0) lo = mid; else hi = mid - 1;
+        }
+        const int s0 = min(max(p.cu_k[lo], 0), p.seqlen_k);
+        const int s1 = min(max(p.cu_k[lo + 1], s0), p.seqlen_k);
+        const int v0 = vt_segment_start(s0, lo);
+        src0 = s0 + (k0 - v0);
+        src_end = k0 >= v0 ? s1 : src0;  // before the first segment's start: zeros
+    }
     const char* src = (const char*)p.v + 2 * (b * p.v_sb + h * p.v_sh);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int key = i * 16 + (t >> 4), c = t & 15;
         i32x4 x = i32x4{0, 0, 0, 0};
-        if (k0 + key < p.seqlen_k) x = *(const i32x4*)(src + (int64_t)(k0 + key) * p.v_rs + c * 16);
+        if (src0 + key < src_end) x = *(const i32x4*)(src + (int64_t)(src0 + key) * p.v_rs + c * 16);
         uint32_t* row = blk + key * 65 + c * 4;
         row[0] = (uint32_t)x.x;
         row[1] = (uint32_t)x.y;
@@ -777,20 +969,36 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
     const int split_tile = blockIdx.x / (kBM / kMergeRows);
     const int row = (blockIdx.x % (kBM / kMergeRows)) * kMergeRows + threadIdx.x / 8;
     const int d0 = (threadIdx.x % 8) * 16;
-    const int tile = p.n_full + split_tile;
+    // Dense: split tile i is tile n_full + i, its piece c in slot
+    // c * split_tiles + i. Planned varlen: merge slot i names a list position
+    // and its piece count (the grid is an upper bound), piece c in slot
+    // i * kQueuePieces + c.
+    int tile = p.n_full + split_tile, n = p.split_n;
+    int64_t slot0 = split_tile, slot_step = p.split_tiles;
+    if (p.vplan != nullptr) {
+        if (split_tile >= p.vplan[kPlanMerges]) return;
+        tile = p.vlist[p.vmerge[2 * split_tile]];
+        n = p.vmerge[2 * split_tile + 1];
+        slot0 = (int64_t)split_tile * kQueuePieces;
+        slot_step = 1;
+    }
     const int qt = tile % p.n_qtiles;
     const int rest = tile / p.n_qtiles;
     const int h = rest % p.heads;
-    const int b = rest / p.heads;
+    int b = rest / p.heads, q0 = 0, sq = p.seqlen_q;
+    if (p.cu_q != nullptr) {
+        q0 = min(max(p.cu_q[b], 0), p.seqlen_q);
+        sq = min(max(p.cu_q[b + 1], q0), p.seqlen_q) - q0;
+        b = 0;
+    }
     const int mq = qt * kBM + row;
-    if (mq >= p.seqlen_q) return;
-    const int n = p.split_n;
+    if (mq >= sq) return;
     float lq[kMaxP];
     f32x4 part[kMaxP][4];
 #pragma unroll
     for (int c = 0; c < kMaxP; ++c) {
         if (c >= n) break;
-        const int64_t pc = (int64_t)c * p.split_tiles + split_tile;
+        const int64_t pc = slot0 + c * slot_step;
         lq[c] = p.ws_lse[pc * kBM + row];
         const f32x4* src = (const f32x4*)(p.ws_o + (pc * kBM + row) * kD + d0);
 #pragma unroll
@@ -815,7 +1023,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
         for (int i = 0; i < 4; ++i) acc[i] += w * part[c][i];
     }
     const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
-    char* ob = (char*)p.o + 2 * (b * p.o_sb + h * p.o_sh + d0) + (int64_t)mq * p.o_rs;
+    char* ob = (char*)p.o + 2 * (b * p.o_sb + h * p.o_sh + d0) + (int64_t)(q0 + mq) * p.o_rs;
     i32x4 w0, w1;
     w0.x = (int)pack_bf16x2(acc[0].x * inv, acc[0].y * inv);
     w0.y = (int)pack_bf16x2(acc[0].z * inv, acc[0].w * inv);
@@ -828,12 +1036,14 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
     *(i32x4*)ob = w0;
     *(i32x4*)(ob + 16) = w1;
     if (p.lse != nullptr && d0 == 0)
-        p.lse[b * p.lse_sb + h * p.lse_sh + mq] = wsum > 0.f ? lse_max + __logf(wsum) : -INFINITY;
+        p.lse[b * p.lse_sb + h * p.lse_sh + q0 + mq] = wsum > 0.f ? lse_max + __logf(wsum) : -INFINITY;
 }
 
 }  // namespace
 
 int attn_fwd_block_m() { return kBM; }
+int attn_fwd_tail_pieces() { return kQueuePieces; }
+int64_t attn_fwd_piece_bytes() { return (int64_t)kBM * (kD + 1) * (int64_t)sizeof(float); }
 int attn_fwd_block_n() { return kBN; }
 int attn_fwd_window_rows() { return kWindowRows > kBM ? kWindowRows : kBM; }
 int attn_fwd_row_margin() { return kBM + kBN * (2 * kStages + 2); }
@@ -912,7 +1122,11 @@ hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
     const int64_t tiles = (int64_t)p.n_qtiles * p.heads * p.n_groups;
     if (tiles <= 0) return hipSuccess;
     int64_t blocks = tiles;
-    if (p.queue != nullptr) {
+    if (p.vplan != nullptr) {
+        // The list, its pieces and the d-major V offsets first.
+        hipLaunchKernelGGL(attn_varlen_plan_kernel, dim3(1), dim3(256), 0, stream, p);
+        blocks = (int64_t)p.ub_tiles + p.plan_cus;
+    } else if (p.queue != nullptr) {
         // With a d-major V copy the transpose kernel zeroes the counter.
         if (p.vt == nullptr) hipLaunchKernelGGL(attn_queue_reset, dim3(1), dim3(64), 0, stream, p.queue);
         blocks = (int64_t)p.n_full + p.queue_blocks;
@@ -920,7 +1134,9 @@ hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
         blocks = (int64_t)p.n_full + (int64_t)p.split_n * p.split_tiles;
     }
     if (p.vt != nullptr) {
-        const dim3 tgrid((unsigned)((p.seqlen_k + kBN - 1) / kBN), (unsigned)p.heads, (unsigned)p.n_groups);
+        // Dense: the keys of the sequence; varlen: every key of the padded rows.
+        const int64_t vt_tiles = (p.seqlen_k + kBN - 1) / kBN + (p.cu_k != nullptr ? p.n_groups : 0);
+        const dim3 tgrid((unsigned)vt_tiles, (unsigned)p.heads, (unsigned)(p.cu_k != nullptr ? 1 : p.n_groups));
         hipLaunchKernelGGL(attn_vt_kernel, tgrid, dim3(256), 0, stream, p);
     }
     const dim3 grid((unsigned)blocks), block(kThreads);
@@ -933,7 +1149,15 @@ hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
     else
         hipLaunchKernelGGL((attn_fwd_kernel<false, false>), grid, block, 0, stream, p);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || p.split_n == 0) return e;
+    if (e != hipSuccess) return e;
+    if (p.vplan != nullptr) {
+        // Every possible merge slot (at most plan_cus split tiles); slots past
+        // the plan's count exit.
+        const dim3 merge_grid((unsigned)(p.plan_cus * (kBM / kMergeRows)));
+        hipLaunchKernelGGL(attn_merge_kernel<4>, merge_grid, dim3(256), 0, stream, p);
+        return hipGetLastError();
+    }
+    if (p.split_n == 0) return e;
     const dim3 merge_grid((unsigned)(p.split_tiles * (kBM / kMergeRows)));
     if (p.split_n <= 4)
         hipLaunchKernelGGL(attn_merge_kernel<4>, merge_grid, dim3(256), 0, stream, p);

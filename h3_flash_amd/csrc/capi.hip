@@ -151,18 +151,48 @@ h3a::SplitPlan attn_plan(const h3a_attn_args* a, const h3a::AttnParams& p, int64
 struct AttnWorkspace {
     h3a::SplitPlan plan;
     int64_t vt_offset;  // 0: no d-major V
-    int64_t vt_rs;      // bytes per row of keys
+    int64_t vt_rs;      // bytes per row of keys (0: no d-major V)
+    // Packed varlen with a device-built work list (ub_tiles > 0): partial
+    // results at 0, the plan's words at plan_offset.
+    int64_t plan_offset;
+    int32_t ub_tiles, cus;
     int64_t total;
 };
 
 AttnWorkspace attn_workspace(const h3a_attn_args* a, const h3a::AttnParams& p, bool allow_vt,
                              int64_t max_workspace = INT64_MAX) {
-    AttnWorkspace w{attn_plan(a, p, max_workspace), 0, 0, 0};
+    AttnWorkspace w{attn_plan(a, p, max_workspace), 0, 0, 0, 0, 0, 0};
     w.total = w.plan.workspace_bytes;
     const int bn = h3a::attn_fwd_block_n();
+    if (a->cu_seqlens_q != nullptr) {
+        // Packed varlen: the work list, the last round's partial results (at
+        // most tail_pieces per CU-round tile), and a d-major V whose segments
+        // are each padded to a multiple of 64 keys.
+        const int cus = device_cus();
+        if (!allow_vt || cus <= 0) return w;
+        const int64_t nseg = a->num_segments, bm = h3a::attn_fwd_block_m();
+        const int64_t grid = (int64_t)p.n_qtiles * p.heads * p.n_groups;
+        int64_t ub = a->heads * ((a->seqlen_q + bm - 1) / bm + nseg);
+        ub = ub < grid ? ub : grid;
+        const int64_t pieces = (int64_t)h3a::attn_fwd_tail_pieces() * cus;
+        const int64_t words = h3a::kPlanWords + ub + 2 * pieces + 2 * cus + 4 * nseg;
+        w.plan_offset = pieces * h3a::attn_fwd_piece_bytes();
+        w.total = w.plan_offset + (4 * words + 255) / 256 * 256;
+        if (w.total > max_workspace) return AttnWorkspace{w.plan, 0, 0, 0, 0, 0, 0};
+        w.ub_tiles = (int32_t)ub;
+        w.cus = cus;
+        const int64_t vt_rs = ((a->seqlen_k + bn - 1) / bn * bn + bn * nseg) * 2;
+        if (a->seqlen_k == 0 || 128 * vt_rs >= kMaxWindow) return w;
+        const int64_t bytes = a->heads * 128 * vt_rs;
+        if (w.total + bytes > max_workspace) return w;
+        w.vt_offset = w.total;
+        w.vt_rs = vt_rs;
+        w.total += bytes;
+        return w;
+    }
     const int64_t vt_rs = (a->seqlen_k + bn - 1) / bn * bn * 2;
     // The d-major V is addressed with 32-bit offsets within a head's block.
-    if (!allow_vt || a->cu_seqlens_q != nullptr || a->seqlen_k == 0 || 128 * vt_rs >= kMaxWindow) return w;
+    if (!allow_vt || a->seqlen_k == 0 || 128 * vt_rs >= kMaxWindow) return w;
     const int64_t offset = (w.total + 255) / 256 * 256;
     const int64_t bytes = a->batch * a->heads * 128 * vt_rs;
     if (offset + bytes > max_workspace) return w;
@@ -248,6 +278,19 @@ int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
     const AttnWorkspace w = attn_workspace(a, p, true);
     if (w.total > 0 && a->workspace != nullptr && a->workspace_bytes >= w.total && ((uintptr_t)a->workspace & 255u) == 0) {
         if (w.plan.split_n != 0) apply_plan(p, w.plan, a->workspace);
+        if (w.ub_tiles > 0) {
+            const int64_t pieces = (int64_t)h3a::attn_fwd_tail_pieces() * w.cus;
+            p.ws_o = (float*)a->workspace;
+            p.ws_lse = p.ws_o + pieces * h3a::attn_fwd_block_m() * 128;
+            int32_t* words = (int32_t*)((char*)a->workspace + w.plan_offset);
+            p.vplan = p.vplan_w = words;
+            p.vlist = p.vlist_w = words + h3a::kPlanWords;
+            p.vpieces = p.vpieces_w = p.vlist_w + w.ub_tiles;
+            p.vmerge = p.vmerge_w = p.vpieces_w + 2 * pieces;
+            p.vscratch = p.vmerge_w + 2 * w.cus;
+            p.ub_tiles = w.ub_tiles;
+            p.plan_cus = w.cus;
+        }
         if (w.vt_rs != 0) {
             p.vt = (char*)a->workspace + w.vt_offset;
             p.vt_rs = (int32_t)w.vt_rs;

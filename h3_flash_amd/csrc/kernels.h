@@ -47,13 +47,33 @@ struct AttnParams {
     // Some view spans 2^31 bytes or more: K / V buffer resources are rebased
     // per window of key tiles.
     int32_t wide;
-    // d-major V (dense launches with a workspace; NULL: V is read as given):
+    // d-major V (launches with a workspace; NULL: V is read as given):
     // attn_vt_kernel writes, per (batch, head), 128 rows of vt_rs bytes with
-    // keys contiguous, zero past seqlen_k up to a multiple of 64 keys.
+    // keys contiguous, zero past seqlen_k up to a multiple of 64 keys; in a
+    // varlen launch segment s starts at key roundup(its first key, 64) + 64 s,
+    // zeros between segments.
     void* vt;
     int64_t vt_sb, vt_sh;  // batch / head strides of vt, in elements
     int32_t vt_rs;         // bytes per head-dim row, a multiple of 128
+    // Packed varlen launches with a workspace: a work list built on the
+    // device by attn_varlen_plan_kernel (NULL: dispatch order, no split).
+    // Workgroups [0, ub_tiles) run the list's whole tiles (ub_tiles bounds
+    // the non-empty tiles); plan_cus more take the last round's pieces.
+    const int32_t* vplan;    // kPlanWords counts and the tail counter
+    const int32_t* vlist;    // tile ids, in run order
+    const int32_t* vpieces;  // per piece: list position, chunk | chunks << 2 | (merge slot + 1) << 5
+    const int32_t* vmerge;   // per merge slot: list position, pieces
+    int32_t* vplan_w;        // the same arrays, written by the planning kernel
+    int32_t* vlist_w;
+    int32_t* vpieces_w;
+    int32_t* vmerge_w;
+    int32_t* vscratch;       // 4 * num_segments words of the planning kernel
+    int32_t ub_tiles;
+    int32_t plan_cus;
 };
+
+// Words of the planned-varlen header (vplan).
+enum : int { kPlanTiles = 0, kPlanFull = 1, kPlanPieces = 2, kPlanMerges = 3, kPlanQueue = 4, kPlanWords = 16 };
 
 // How the query tiles of a dense launch are spread over the CUs.
 struct SplitPlan {
@@ -72,6 +92,10 @@ constexpr int64_t kStaticScratchBytes = H3A_NOALLOC_SCRATCH_BYTES;
 hipError_t attn_static_scratch(void** ptr);
 
 int attn_fwd_block_m();
+// Most key-range pieces per tile of a tail, and the workspace bytes of one
+// piece's fp32 partial O and LSE.
+int attn_fwd_tail_pieces();
+int64_t attn_fwd_piece_bytes();
 int attn_fwd_block_n();
 // Rows one buffer resource of the kernel spans from its base (a query tile, or
 // a window of key tiles in the wide form); their bytes must stay below 2^31.

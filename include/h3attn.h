@@ -90,9 +90,8 @@ extern "C" {
  *
  * Rows with no key (seqlen_k == 0) produce O = 0 and LSE = -inf.
  *
- * Workspace (dense inputs only), h3a_attn_fwd_workspace_size(args) bytes of
- * device memory at `workspace` (256-byte aligned, contents on entry
- * irrelevant), used for two things:
+ * Workspace: h3a_attn_fwd_workspace_size(args) bytes of device memory at
+ * `workspace` (256-byte aligned, contents on entry irrelevant), used for:
  *   - the split tail: with more query tiles (256 rows of one head) than the
  *     GPU has CUs, the tiles of the last round run as key-range pieces that
  *     workgroups take from a counter in the workspace as CUs free up; with
@@ -104,7 +103,13 @@ extern "C" {
  *   - a d-major copy of V (per batch and head, 128 rows of keys padded with
  *     zeros to a multiple of 64), written by a transpose kernel at the start
  *     of the call, from which the attention kernel reads each PV fragment
- *     with one 16-byte LDS read.
+ *     with one 16-byte LDS read;
+ *   - packed varlen: a work list planned on the device from cu_seqlens by a
+ *     one-workgroup kernel at the start of the call (non-empty tiles,
+ *     longest segments first; the last round's tiles as key-range pieces
+ *     taken from a counter, merged as above), and the d-major V with each
+ *     segment padded to 64 keys. Any cu_seqlens contents keep every access
+ *     in bounds; offsets that do not ascend give undefined rows.
  * With a NULL or smaller workspace every tile runs whole on V as given. The
  * results differ only by rounding. Calls sharing one workspace must be
  * ordered (same stream).

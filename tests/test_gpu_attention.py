@@ -444,13 +444,61 @@ def test_c5_packed_varlen_sampled_rows():
     rows = _sample_rows(q.shape[1], 96, 19, extra=(49919, 49920, 49921, 51199, 51200, 51207, 51215))
     ref_o, ref_l = sdpa_rows(q.cpu(), k.cpu(), v.cpu(), rows, cu_seqlens=cu)
     assert_parity(out[:, rows.to(DEV)].cpu(), lse[:, :, rows.to(DEV)].cpu(), ref_o, ref_l, "c5")
-    # the audio segment must not see video keys: compare with a standalone run
+    # the audio segment must not see video keys: compare with a standalone
+    # run, bit for bit on the same kernel form (split_tail=False: dispatch
+    # order, V as given) and within the tolerance for the default planned
+    # launch (d-major V, work list)
     a0 = 49920
     oa_, la_ = flash_attn_func(
         q[:, a0:].contiguous(), k[:, a0:].contiguous(), v[:, a0:].contiguous(), split_tail=False
     )
+    ou, lu = flash_attn_func(q, k, v, cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV), max_seqlen_q=49920,
+                             split_tail=False)
     torch.cuda.synchronize()
-    assert torch.equal(oa_, out[:, a0:]) and torch.equal(la_, lse[:, :, a0:])
+    assert torch.equal(oa_, ou[:, a0:]) and torch.equal(la_, lu[:, :, a0:])
+    assert_parity(out[:, a0:].cpu(), lse[:, :, a0:].cpu(), oa_.float().cpu(), la_.cpu(), "c5 audio")
+
+
+@pytest.mark.parametrize(
+    "segments",
+    [
+        (49_920, 1_296),
+        (1_024,) * 48,
+        (40_000, 40_000),
+        (49_920, 30_000, 20_000, 1_296),
+        (0, 700, 0, 3_000, 5),
+        (300,),
+    ],
+)
+def test_planned_varlen_segmentations(segments):
+    """Packed varlen launches with a workspace run a work list planned on the
+    device (longest segments first, the last round's tiles cut into pieces
+    from a counter) and a d-major V with each segment padded to 64 keys. The
+    result must match the unplanned launch (dispatch order, V as given)
+    within the path's tolerance, sampled rows the oracle, and be the same
+    bits on every run."""
+
+    print(f"case: planned varlen {segments}", flush=True)
+    H = 5
+    S = sum(segments)
+    g = torch.Generator().manual_seed(len(segments) * 7 + S)
+    q, k, v = (torch.randn((1, S, H, 128), generator=g).to(torch.bfloat16) for _ in range(3))
+    bounds = [0]
+    for n in segments:
+        bounds.append(bounds[-1] + n)
+    cu = torch.tensor(bounds, dtype=torch.int32, device=DEV)
+    kw = {"cu_seqlens_q": cu, "cu_seqlens_k": cu, "max_seqlen_q": max(max(segments), 1)}
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    out, lse = flash_attn_func(qd, kd, vd, **kw)
+    out2, lse2 = flash_attn_func(qd, kd, vd, **kw)
+    ou, lu = flash_attn_func(qd, kd, vd, split_tail=False, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2) and torch.equal(lse, lse2)
+    assert_parity(out.cpu(), lse.cpu(), ou.float().cpu(), lu.cpu(), f"planned vs unplanned {segments}")
+    rows = torch.unique(torch.tensor([b for b in bounds[:-1]] + [b - 1 for b in bounds[1:] if b > 0] + [S // 2]))
+    rows = rows[(rows >= 0) & (rows < S)]
+    ref_o, ref_l = sdpa_rows(q, k, v, rows, cu_seqlens=cu.cpu())
+    assert_parity(out[:, rows.to(DEV)].cpu(), lse[:, :, rows.to(DEV)].cpu(), ref_o, ref_l, f"oracle {segments}")
 
 
 @pytest.mark.parametrize("name", ["c2", "c3", "c4"])

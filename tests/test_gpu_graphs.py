@@ -1,10 +1,12 @@
 """The hot path captured in a HIP graph (torch.cuda.CUDAGraph), the way a
 serving loop would replay it: the prologue, the attention with its
 split-tail workspace and merge kernel, the attention's dynamic tail (its
-counter is reset by a kernel recorded in the graph), and a row fusion. Each replay runs on
-new inputs written into the captured buffers by eager work, and must equal
-the eager launches on the same inputs bit for bit (same kernels, same
-launch shapes, deterministic)."""
+counter is reset by a kernel recorded in the graph), a packed varlen launch
+whose work list is planned on the device (the segmentation changes between
+replays: the recorded planning kernel reads the new offsets), and a row
+fusion. Each replay runs on new inputs written into the captured buffers by
+eager work, and must equal the eager launches on the same inputs bit for bit
+(same kernels, same launch shapes, deterministic)."""
 
 from __future__ import annotations
 
@@ -32,6 +34,10 @@ def test_prologue_attention_and_fusion_replay_in_a_graph():
     q_raw, k_raw, v = (torch.empty((1, S, H, D), dtype=torch.bfloat16, device=DEV) for _ in range(3))
     # 320 tiles: the dynamic-tail path (counter reset, queued pieces, merge)
     q2, k2, v2 = (torch.empty((1, 16384, 5, D), dtype=torch.bfloat16, device=DEV) for _ in range(3))
+    # packed varlen over 6,000 rows; segment offsets rewritten before every replay
+    q3, k3, v3 = (torch.empty((1, 6000, 5, D), dtype=torch.bfloat16, device=DEV) for _ in range(3))
+    cu = torch.tensor([0, 4000, 6000], dtype=torch.int32, device=DEV)
+    segmentations = ([0, 4000, 6000], [0, 1000, 6000], [0, 5999, 6000], [0, 0, 6000], [0, 3000, 6000])
     x = torch.empty((1, 512, C), dtype=torch.bfloat16, device=DEV)
     w = torch.ones(D, dtype=torch.bfloat16, device=DEV)
     wm = torch.empty(C, dtype=torch.bfloat16, device=DEV)
@@ -47,9 +53,10 @@ def test_prologue_attention_and_fusion_replay_in_a_graph():
         full, full_lse = flash_attn_func(q, k, v)
         y = fused_rmsnorm_modulate(x, wm, table[:, :C], table[:, C:], index, 1e-5)
         tail_o, tail_l = flash_attn_func(q2, k2, v2)
-        return o, l, full, full_lse, y, tail_o, tail_l
+        var_o, var_l = flash_attn_func(q3, k3, v3, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=6000)
+        return o, l, full, full_lse, y, tail_o, tail_l, var_o, var_l
 
-    _fill([q_raw, k_raw, v, x, wm, table, q2, k2, v2], 0)
+    _fill([q_raw, k_raw, v, x, wm, table, q2, k2, v2, q3, k3, v3], 0)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -62,12 +69,13 @@ def test_prologue_attention_and_fusion_replay_in_a_graph():
     torch.cuda.synchronize()
 
     for replay in range(4):
-        _fill([q_raw, k_raw, v, x, wm, table, q2, k2, v2], 100 + replay)
+        _fill([q_raw, k_raw, v, x, wm, table, q2, k2, v2, q3, k3, v3], 100 + replay)
+        cu.copy_(torch.tensor(segmentations[replay + 1], dtype=torch.int32))
         eager = [t.clone() for t in step()]
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
-        names = ("merged", "merged_lse", "attn", "lse", "modulate", "tail_attn", "tail_lse")
+        names = ("merged", "merged_lse", "attn", "lse", "modulate", "tail_attn", "tail_lse", "varlen", "varlen_lse")
         for name, got, want in zip(names, captured, eager):
             assert torch.equal(got, want), f"replay {replay}: {name} differs from the eager launch"
     # the merge of the two key halves is the full attention within the path's tolerance
