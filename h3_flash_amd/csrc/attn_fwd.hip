@@ -72,7 +72,10 @@ constexpr float kRecomputeLimit = 0x1p64f;
 // the view is.
 constexpr int kWindowRows = kBN * 9;
 constexpr int kQueuePieces = 4;                  // key-range pieces per tile of a dynamic tail
-constexpr int kQueueMinKeyTiles = 16;            // fewest key tiles in such a piece
+// Fewest key tiles in such a piece: each piece pays a pipeline fill and
+// drain and a partial result, which short pieces do not recover (8 x 8,192-row
+// segments at 5 heads cut into pieces of 32 key tiles ran 5% slower).
+constexpr int kQueueMinKeyTiles = 48;
 
 static_assert(kDmaPerTile == 2, "vmcnt accounting below assumes 2 K + 2 V loads per iteration");
 static_assert(kStages == 4, "the pipeline below is unrolled over four stages");
@@ -465,9 +468,12 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int chu
                     const int e1 = ((k - kFirstExp + 1) * 32) / (kSlices - kFirstExp);
 #pragma unroll
                     for (int e = e0; e < e1; ++e) {
+                        // The sum and the bf16 pair take the previous score, so
+                        // no instruction waits on the exp just issued (the
+                        // order of the fp32 sum is unchanged).
                         pe[e] = fast_exp2(__builtin_fmaf(s_in[e >> 4][e & 15], c, -mc));
-                        lsum = e == 0 ? pe[e] : lsum + pe[e];  // fp32: l feeds the LSE
-                        if (e & 1) pn[e >> 1] = pack_bf16x2(pe[e - 1], pe[e]);
+                        if (e >= 1) lsum = e == 1 ? pe[0] : lsum + pe[e - 1];  // fp32: l feeds the LSE
+                        if (e >= 2 && !(e & 1)) pn[(e - 1) >> 1] = pack_bf16x2(pe[e - 2], pe[e - 1]);
                     }
                 }
             }
@@ -502,6 +508,8 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int chu
             }
         }
         if constexpr (kSM != 0) {
+            lsum += pe[31];
+            pn[15] = pack_bf16x2(pe[30], pe[31]);
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc)
                 pout[cc] = __builtin_bit_cast(bf16x8, i32x4{(int)pn[4 * cc], (int)pn[4 * cc + 1], (int)pn[4 * cc + 2],
@@ -688,12 +696,12 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // static split (fewer tiles than CUs, n_full == 0) gives every workgroup
     // one piece, each XCD a contiguous range of them.
     // Packed varlen launches with a work list (vplan) run the list's whole
-    // rounds the same way, XCD-contiguous over list positions, and take the
-    // last round's pieces from a counter. Without a list they keep dispatch
-    // order (tile i is workgroup i): tiles past a short segment's end exit at
-    // once, and in dispatch order they spread over all XCDs (contiguous
-    // ranges gave a few XCDs nearly only empty tiles: the 49,920 + 1,296
-    // two-segment batch ran at half speed).
+    // rounds in dispatch order and take the last round's pieces from a
+    // counter. Without a list they keep dispatch order too (tile i is
+    // workgroup i): tiles past a short segment's end exit at once, and in
+    // dispatch order they spread over all XCDs (contiguous ranges gave a few
+    // XCDs nearly only empty tiles: the 49,920 + 1,296 two-segment batch ran
+    // at half speed).
     const int bid = blockIdx.x;
     int tile = bid, chunk = -1, chunks = 1, slot = -1;
     const bool planned = p.vplan != nullptr;
@@ -701,10 +709,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // of the last round's tiles from a counter, one at a time.
     const bool queued = planned ? bid >= p.ub_tiles : p.queue != nullptr && bid >= p.n_full;
     if (planned && !queued) {
-        const int n_full = p.vplan[kPlanFull];
-        if (bid >= n_full) return;
-        const int pos = (n_full & 7) == 0 ? (bid & 7) * (n_full >> 3) + (bid >> 3) : bid;
-        tile = __builtin_amdgcn_readfirstlane(p.vlist[pos]);  // uniform: the addressing is scalar
+        // Dispatch order over the list: its tiles differ in length (longest
+        // first), and round-robin over the XCDs gives every XCD an even share
+        // of each length (XCD-contiguous ranges gave XCD 0 all the longest).
+        if (bid >= p.vplan[kPlanFull]) return;
+        tile = __builtin_amdgcn_readfirstlane(p.vlist[bid]);  // uniform: the addressing is scalar
     } else if (p.cu_q == nullptr && !queued) {
         const int nb = p.queue != nullptr ? p.n_full : (int)gridDim.x;
         const int xcd = bid & 7, local = bid >> 3, per = nb >> 3, rem = nb & 7;
@@ -791,33 +800,34 @@ __device__ __forceinline__ int block_scan(int v, int* buf, int* total) {
 
 __global__ __launch_bounds__(256) void attn_varlen_plan_kernel(AttnParams p) {
     __shared__ int scan[256];
-    __shared__ int lk_s[kPlanSortMax];
+    // Per-segment arrays: in LDS up to kPlanSortMax segments (the planner is
+    // a chain of dependent accesses, so their latency is its time), in the
+    // workspace beyond.
+    __shared__ int lds_seg[4 * kPlanSortMax];
     const int t = threadIdx.x;
     const int nseg = p.n_groups, heads = p.heads, nq = p.n_qtiles, cus = p.plan_cus;
     int* const info = p.vplan_w;
     int* const list = p.vlist_w;
     int* const pieces = p.vpieces_w;
     int* const merge = p.vmerge_w;
-    int* const segq = p.vscratch;
+    const bool sorted = nseg <= kPlanSortMax;
+    int* const segq = sorted ? lds_seg : p.vscratch;
     int* const segk = segq + nseg;
     int* const order = segk + nseg;
     int* const base = order + nseg;
-    const bool sorted = nseg <= kPlanSortMax;
     for (int i = t; i < nseg; i += 256) {
         const int q0 = min(max(p.cu_q[i], 0), p.seqlen_q);
         const int k0 = min(max(p.cu_k[i], 0), p.seqlen_k);
         segq[i] = min(max(p.cu_q[i + 1], q0), p.seqlen_q) - q0;
-        const int lk = min(max(p.cu_k[i + 1], k0), p.seqlen_k) - k0;
-        segk[i] = lk;
-        if (sorted) lk_s[i] = lk;
+        segk[i] = min(max(p.cu_k[i + 1], k0), p.seqlen_k) - k0;
     }
     __syncthreads();
     for (int i = t; i < nseg; i += 256) {
         int r = i;
         if (sorted) {
-            const int li = lk_s[i];
+            const int li = segk[i];
             r = 0;
-            for (int j = 0; j < nseg; ++j) r += (lk_s[j] > li) | ((lk_s[j] == li) & (j < i));
+            for (int j = 0; j < nseg; ++j) r += (segk[j] > li) | ((segk[j] == li) & (j < i));
         }
         order[r] = i;
     }

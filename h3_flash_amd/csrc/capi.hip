@@ -24,6 +24,13 @@ int fail(int code, const char* fmt, ...) {
 }
 
 constexpr int64_t kMaxWindow = (int64_t)1 << 31;  // buffer offsets are 32-bit
+// The d-major V copy costs a pass over V (about 25 us at 5 heads x 49,920
+// keys) and saves about 1.9% of the attention: it pays from about 14k keys
+// per sequence (segment) on; below that V is read as given.
+constexpr int64_t kVtMinKeys = 16384;
+// A planned varlen launch (device-built work list with a balanced last
+// round) pays for its planning launch with segments of this many rows.
+constexpr int64_t kPlanMinSegment = 4096;
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 bool aligned4(const void* p) { return ((uintptr_t)p & 3u) == 0; }
@@ -168,8 +175,10 @@ AttnWorkspace attn_workspace(const h3a_attn_args* a, const h3a::AttnParams& p, b
         // Packed varlen: the work list, the last round's partial results (at
         // most tail_pieces per CU-round tile), and a d-major V whose segments
         // are each padded to a multiple of 64 keys.
+        // Only for segments long enough that a balanced last round pays for
+        // the planning launch (max_seqlen_q bounds them).
         const int cus = device_cus();
-        if (!allow_vt || cus <= 0) return w;
+        if (!allow_vt || cus <= 0 || a->max_seqlen_q < kPlanMinSegment) return w;
         const int64_t nseg = a->num_segments, bm = h3a::attn_fwd_block_m();
         const int64_t grid = (int64_t)p.n_qtiles * p.heads * p.n_groups;
         int64_t ub = a->heads * ((a->seqlen_q + bm - 1) / bm + nseg);
@@ -182,7 +191,7 @@ AttnWorkspace attn_workspace(const h3a_attn_args* a, const h3a::AttnParams& p, b
         w.ub_tiles = (int32_t)ub;
         w.cus = cus;
         const int64_t vt_rs = ((a->seqlen_k + bn - 1) / bn * bn + bn * nseg) * 2;
-        if (a->seqlen_k == 0 || 128 * vt_rs >= kMaxWindow) return w;
+        if (a->seqlen_k == 0 || a->max_seqlen_q < kVtMinKeys || 128 * vt_rs >= kMaxWindow) return w;
         const int64_t bytes = a->heads * 128 * vt_rs;
         if (w.total + bytes > max_workspace) return w;
         w.vt_offset = w.total;
@@ -192,7 +201,7 @@ AttnWorkspace attn_workspace(const h3a_attn_args* a, const h3a::AttnParams& p, b
     }
     const int64_t vt_rs = (a->seqlen_k + bn - 1) / bn * bn * 2;
     // The d-major V is addressed with 32-bit offsets within a head's block.
-    if (!allow_vt || a->seqlen_k == 0 || 128 * vt_rs >= kMaxWindow) return w;
+    if (!allow_vt || a->seqlen_k < kVtMinKeys || 128 * vt_rs >= kMaxWindow) return w;
     const int64_t offset = (w.total + 255) / 256 * 256;
     const int64_t bytes = a->batch * a->heads * 128 * vt_rs;
     if (offset + bytes > max_workspace) return w;

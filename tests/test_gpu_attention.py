@@ -364,8 +364,9 @@ def test_workspace_plan_on_this_device():
 
     per_piece = 256 * 129 * 4  # a multiple of 256
 
-    def vt(B, S, H):  # d-major V: 128 rows of keys per (batch, head), padded to 64 keys
-        return B * H * 128 * ((S + 63) // 64 * 64) * 2
+    def vt(B, S, H):  # d-major V: 128 rows of keys per (batch, head), padded to 64 keys,
+        # for sequences of 16,384 keys or more (shorter ones read V as given)
+        return B * H * 128 * ((S + 63) // 64 * 64) * 2 if S >= 16384 else 0
 
     def total(split, B, S, H):  # split data, 256-byte aligned, then the d-major V
         return (split + 255) // 256 * 256 + vt(B, S, H)
@@ -374,14 +375,17 @@ def test_workspace_plan_on_this_device():
         # more tiles than CUs: the last round's tiles become 4 pieces each in
         # the dynamic tail, plus 256 bytes for its counter
         assert need(1, 49920, 5) == total(4 * 207 * per_piece + 256, 1, 49920, 5)  # 975 tiles: 768 whole
-        assert need(1, 256 * 40, 36) == total(4 * 160 * per_piece + 256, 1, 256 * 40, 36)  # 1440 tiles
+        # 1440 tiles of 160 key tiles: 3 pieces each (at least 48 key tiles per piece)
+        assert need(1, 256 * 40, 36) == total(3 * 160 * per_piece + 256, 1, 256 * 40, 36)
         assert need(1, 256 * 128, 8) == total(4 * 256 * per_piece + 256, 1, 256 * 128, 8)  # 1024 tiles
         # one partial round: static pieces when it keeps under 70% of the CUs busy
         assert need(1, 4096, 4) == total(4 * 64 * per_piece, 1, 4096, 4)  # 64 tiles, 4 pieces each
         assert need(1, 256 * 200, 1) == vt(1, 256 * 200, 1)  # 200 tiles (78%): whole
-        # two key tiles: 2 pieces; the d-major V pads 70 keys to 128
-        assert need(1, 70, 1) == total(2 * per_piece, 1, 70, 1) and vt(1, 70, 1) == vt(1, 128, 1)
-    assert need(1, 64, 1) == vt(1, 64, 1)  # one key tile: nothing to split, only the d-major V
+        # two key tiles: 2 pieces (70 keys: no d-major V)
+        assert need(1, 70, 1) == total(2 * per_piece, 1, 70, 1) == 2 * per_piece
+        # 201 tiles (78%): whole; the d-major V pads 51,201 keys to 51,264
+        assert need(1, 51201, 1) == need(1, 51264, 1) == vt(1, 51264, 1) == 128 * 51264 * 2
+    assert need(1, 64, 1) == 0  # one key tile: nothing to split, no d-major V
 
 
 def test_unsupported_requests_raise():
