@@ -73,8 +73,13 @@ def build_library(verbose: bool = False, extra_flags: tuple[str, ...] = ()) -> P
     flags = [f for f in HIPCC_FLAGS if f != "-shared"]
     with tempfile.TemporaryDirectory(prefix="h3a_build_") as objdir:
         objects = [str(Path(objdir) / (Path(name).stem + ".o")) for name in SOURCES]
+        # A fixed compilation-unit id per source: by default it hashes the
+        # invocation, whose object path is a fresh temporary directory, and
+        # the library's bytes (its sha256, which the bench matches against
+        # profiled counters) would change with every build.
         compiles = [
-            [compiler, *flags, *extra_flags, f"-I{INCLUDE_DIR}", "-c", str(CSRC_DIR / name), "-o", obj]
+            [compiler, *flags, *extra_flags, f"-cuid=h3a_{Path(name).stem}", f"-I{INCLUDE_DIR}", "-c", str(CSRC_DIR / name),
+             "-o", obj]
             for name, obj in zip(SOURCES, objects)
         ]
         workers = max(1, min(len(compiles), os.cpu_count() or 1, 8))
