@@ -76,6 +76,9 @@ constexpr int kQueuePieces = 4;                  // key-range pieces per tile of
 // drain and a partial result, which short pieces do not recover (8 x 8,192-row
 // segments at 5 heads cut into pieces of 32 key tiles ran 5% slower).
 constexpr int kQueueMinKeyTiles = 48;
+// Key tiles from which a 4-way queued split is graded (its small pieces keep
+// 32 key tiles or more).
+constexpr int kGradedMinKeyTiles = 256;
 
 static_assert(kDmaPerTile == 2, "vmcnt accounting below assumes 2 K + 2 V loads per iteration");
 static_assert(kStages == 4, "the pipeline below is unrolled over four stages");
@@ -143,7 +146,8 @@ __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory
 // taken in the order that swaps bits 2 and 3 of the key index (keyperm), so
 // that the eight keys a lane holds in P^T are consecutive.
 template <bool kWide, bool kVT>
-__device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int chunk, int chunks, int slot) {
+__device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int chunk, int chunks, int slot,
+                                          bool graded = false) {
     __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
     // V stages 0..3 first, then K stages 0..3: with a per-lane base in a VGPR
     // every fragment read offset then fits the 16-bit ds_read immediate.
@@ -183,9 +187,18 @@ __device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int chu
     const int m0 = qt * kBM;
     if (m0 >= sq) return;  // whole workgroup: tile beyond this segment
     if (chunk >= 0) {
-        // Piece c of n covers key tiles [c*nkt/n, (c+1)*nkt/n).
+        // Piece c of n covers key tiles [c*nkt/n, (c+1)*nkt/n). Graded
+        // pieces (a queue's 4-way split of long key ranges) cover 3/8, 3/8,
+        // 1/8 and 1/8 instead: the queue hands out every tile's first pieces
+        // before any last one, so the pieces left at the end of the launch
+        // are small and the CUs finish closer together.
         const int nkt = (sk + kBN - 1) / kBN;
-        const int kt0 = chunk * nkt / chunks, kt1 = (chunk + 1) * nkt / chunks;
+        int kt0 = chunk * nkt / chunks, kt1 = (chunk + 1) * nkt / chunks;
+        if (graded && chunks == 4 && nkt >= kGradedMinKeyTiles) {
+            auto edge = [](int c) { return c < 2 ? 3 * c : c + 4; };  // 0, 3, 6, 7, 8 eighths
+            kt0 = edge(chunk) * nkt / 8;
+            kt1 = edge(chunk + 1) * nkt / 8;
+        }
         k0 += kt0 * kBN;
         sk = min(sk - kt0 * kBN, (kt1 - kt0) * kBN);
     }
@@ -757,11 +770,11 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         } else {
             if ((unsigned)piece >= (unsigned)(p.split_n * p.split_tiles)) return;
             tile = p.n_full + piece % p.split_tiles;
-            chunk = piece / p.split_tiles;
+            chunk = piece / p.split_tiles;  // chunk-major: every tile's first pieces first
             chunks = p.split_n;
             slot = piece;
         }
-        attn_tile<kWide, kVT>(p, tile, chunk, chunks, slot);
+        attn_tile<kWide, kVT>(p, tile, chunk, chunks, slot, !planned);
     }
 }
 
