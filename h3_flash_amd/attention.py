@@ -33,6 +33,7 @@ from typing import Any
 import torch
 
 from . import _ext
+from .audit import gate_qknorm_rope
 from .prologue import fused_qk_norm_rope
 
 __all__ = [
@@ -292,6 +293,10 @@ class DenseMiniMaxH3Processor:
     def __init__(self, *, kernel: Callable[..., Any] | None = None) -> None:
         self.kernel = load_kernel() if kernel is None else kernel
         self.calls = 0
+        # Set by install_dense_hip on the first module: the install record,
+        # whose "gate" receives the fused prologue's error on the first call
+        # (transformer.py:174-190).
+        self._runtime: dict[str, Any] | None = None
 
     def __call__(
         self,
@@ -327,6 +332,8 @@ class DenseMiniMaxH3Processor:
                 )
             cos, sin = rotary_emb
             query, key = fused_qk_norm_rope(query, key, nq[0], nk[0], cos, sin, nq[1], nk[1])
+            if self._runtime is not None and "qknorm_partial_rope" not in self._runtime["gate"]:
+                self._runtime["gate"]["qknorm_partial_rope"] = gate_qknorm_rope(attn, hidden_states, query, cos, sin)
         output = self.kernel(query, key, value, causal=False)
         if isinstance(output, tuple):
             output = output[0]
@@ -343,6 +350,11 @@ def install_dense_hip(transformer: Any, attention_class: type | None = None) -> 
     by ``attention_class`` when given, else by the class name
     ``MiniMaxH3Attention``. Raises RuntimeError when none is found or the
     library is missing.
+
+    The returned record is live: its ``"gate"`` dict receives, on the first
+    rotary call of the first module, the error metrics of the fused q/k
+    RMSNorm + RoPE against the eager composition, as the reference's fused
+    runtime records them (transformer.py:174-190).
     """
 
     kernel = load_kernel()
@@ -361,9 +373,12 @@ def install_dense_hip(transformer: Any, attention_class: type | None = None) -> 
     if not processors:
         raise RuntimeError("no MiniMax H3 attention modules found")
     transformer._h3_flash_dense_hip_processors = processors
-    return {
+    record = {
         "backend": "hip_gfx950",
         "semantics": "dense",
         "processor_count": len(processors),
         **provenance(),
+        "gate": {},
     }
+    processors[0]._runtime = record
+    return record

@@ -191,6 +191,10 @@ def test_install_sets_one_shared_kernel_on_every_module() -> None:
     assert record["abi_version"] == _ext.ABI_VERSION
     kernels = {id(block.processor.kernel) for block in transformer.blocks}
     assert len(kernels) == 1
+    # the first module's processor fills the record's gate on its first rotary call
+    assert record["gate"] == {}
+    assert transformer.blocks[0].processor._runtime is record
+    assert all(b.processor._runtime is None for b in transformer.blocks[1:])
     assert transformer._h3_flash_dense_hip_processors == [b.processor for b in transformer.blocks]
 
 

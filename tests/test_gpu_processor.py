@@ -104,3 +104,13 @@ def test_install_and_run_every_module():
     torch.cuda.synchronize()
     assert torch.isfinite(x.float()).all()
     assert [b.processor.calls for b in t.blocks] == [1, 1]
+    # the install record carries the fused prologue's first-block gate
+    # (transformer.py:174-190): the HIP q against norm_q then eager RoPE,
+    # which rounds once more (after the norm), so up to about two bf16 ulps
+    gate = record["gate"]["qknorm_partial_rope"]
+    assert set(gate) == {"max_abs", "mean_abs", "relative_l2", "cosine"}
+    assert gate["max_abs"] <= 0.05 and gate["mean_abs"] <= 2e-3, gate
+    assert gate["relative_l2"] <= 1e-2 and gate["cosine"] > 0.9999, gate
+    with torch.no_grad():
+        t.blocks[0](x, rotary_emb=(cos, sin))
+    assert record["gate"]["qknorm_partial_rope"] is gate  # measured once

@@ -26,8 +26,10 @@ def _t(values) -> torch.Tensor:
     return torch.tensor(values, dtype=torch.float32)
 
 
-def metric_checks(metrics) -> list[str]:
-    """Run every case on ``metrics(actual, reference)``; return the failed ones."""
+def metric_checks(metrics, tol_floor: float = 0.0) -> list[str]:
+    """Run every case on ``metrics(actual, reference)``; return the failed
+    ones. ``tol_floor`` raises every relative tolerance to at least that much
+    (1e-6 for metrics computed in fp32 rather than float64)."""
 
     failed = []
 
@@ -38,6 +40,7 @@ def metric_checks(metrics) -> list[str]:
             failed.append(name)
 
     def close(x, y, tol=1e-9):
+        tol = max(tol, tol_floor)
         assert math.isclose(x, y, rel_tol=tol, abs_tol=tol), (x, y)
 
     def spike():
@@ -181,3 +184,43 @@ def _mutant(kind: str):
 )
 def test_planted_metric_mistakes_are_caught(kind: str) -> None:
     assert metric_checks(_mutant(kind)) != []
+
+
+def test_product_audit_metrics_follow_the_pinned_oracle() -> None:
+    """h3_flash_amd.audit.error_metrics (the install record's gate) computes
+    the same quantities as the pinned oracle, and passes the same cases to
+    fp32 precision (it works in fp32, as the reference's gate does)."""
+
+    from h3_flash_amd.audit import error_metrics as audit_metrics
+
+    def as_oracle(actual, reference):
+        m = audit_metrics(actual, reference)
+        m["finite"] = bool(torch.isfinite(actual.float()).all())
+        return m
+
+    assert metric_checks(as_oracle, tol_floor=1e-6) == []
+    g = torch.Generator().manual_seed(3)
+    a, r = torch.randn(4, 33, generator=g), torch.randn(4, 33, generator=g)
+    got, want = audit_metrics(a, r), error_metrics(a, r)
+    for key in ("max_abs", "mean_abs", "relative_l2", "cosine"):
+        assert math.isclose(got[key], want[key], rel_tol=1e-5, abs_tol=1e-7), key
+
+
+def test_eager_rope_of_the_gate_matches_the_prologue_oracle() -> None:
+    """The gate's eager side (RMSNorm, then rotate-half RoPE over the first R
+    columns) equals the oracle's fused closed form in fp32, for R = D and for
+    a partial R with pass-through columns."""
+
+    from h3_flash_amd.audit import eager_qknorm_rope
+    from oracle.qknorm_rope import qknorm_rope_reference
+
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(1, 6, 2, 128, generator=g)
+    w = 1.0 + 0.1 * torch.randn(128, generator=g)
+    for R in (128, 96):
+        theta = torch.rand(6, R // 2, generator=g) * 6.0
+        cos, sin = torch.cos(torch.cat((theta, theta), -1)), torch.sin(torch.cat((theta, theta), -1))
+        normed = functional.rms_norm(x, (128,), w, 1e-6)
+        got = eager_qknorm_rope(normed, cos, sin)
+        want = qknorm_rope_reference(x, w, cos, sin, 1e-6, out_dtype=None)
+        assert (got - want).abs().max().item() < 1e-5, R
