@@ -1,7 +1,6 @@
 """ctypes binding of the C ABI in ``include/h3attn.h``.
 
-The structures below mirror ``h3a_attn_args`` and ``h3a_qknorm_rope_args``
-field for field. Loading fails loudly (``RuntimeError``) when the library has
+The structures below mirror the header's argument structs field for field. Loading fails loudly (``RuntimeError``) when the library has
 not been built: there is no other implementation behind these entry points.
 """
 
@@ -14,7 +13,7 @@ from pathlib import Path
 
 from ._build import LIB_PATH
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 H3A_OK = 0
 H3A_EINVAL = -1
@@ -237,6 +236,44 @@ class AttnMergeArgs(ctypes.Structure):
     ]
 
 
+H3A_PROJ_PLAIN = 0
+H3A_PROJ_QKNORM_ROPE = 1
+H3A_PROJ_MAX_SECTIONS = 3
+
+
+class ProjSection(ctypes.Structure):
+    _fields_ = [
+        ("weight", ctypes.c_void_p),
+        ("weight_stride", ctypes.c_int64),
+        ("n", ctypes.c_int64),
+        ("bias", ctypes.c_void_p),
+        ("y", ctypes.c_void_p),
+        ("y_stride", ctypes.c_int64),
+        ("mode", ctypes.c_int32),
+        ("norm_weight", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+    ]
+
+
+class ProjArgs(ctypes.Structure):
+    _fields_ = [
+        ("abi_version", ctypes.c_int32),
+        ("x", ctypes.c_void_p),
+        ("x_stride", ctypes.c_int64),
+        ("m", ctypes.c_int64),
+        ("k", ctypes.c_int64),
+        ("head_dim", ctypes.c_int64),
+        ("num_sections", ctypes.c_int32),
+        ("sections", ProjSection * H3A_PROJ_MAX_SECTIONS),
+        ("cos", ctypes.c_void_p),
+        ("sin", ctypes.c_void_p),
+        ("table_stride", ctypes.c_int64),
+        ("rotary_dim", ctypes.c_int64),
+        ("seqlen", ctypes.c_int64),
+        ("rotate_half_tables", ctypes.c_int32),
+    ]
+
+
 # Every function the header declares, with its ctypes signature.
 SIGNATURES = {
     "h3a_attn_fwd": (ctypes.c_int, [ctypes.POINTER(AttnArgs), ctypes.c_void_p]),
@@ -253,6 +290,7 @@ SIGNATURES = {
     ),
     "h3a_swiglu": (ctypes.c_int, [ctypes.POINTER(SwigluArgs), ctypes.c_void_p]),
     "h3a_attn_merge": (ctypes.c_int, [ctypes.POINTER(AttnMergeArgs), ctypes.c_void_p]),
+    "h3a_proj_gemm": (ctypes.c_int, [ctypes.POINTER(ProjArgs), ctypes.c_void_p]),
     "h3a_last_error": (ctypes.c_char_p, []),
     "h3a_abi_version": (ctypes.c_int, []),
 }

@@ -679,4 +679,108 @@ int h3a_attn_merge(const h3a_attn_merge_args* a, void* stream) {
     return H3A_OK;
 }
 
+int h3a_proj_gemm(const h3a_proj_args* a, void* stream) {
+    g_err[0] = '\0';
+    const char* fn = "h3a_proj_gemm";
+    if (a == nullptr) return fail(H3A_EINVAL, "%s: args is NULL", fn);
+    if (a->abi_version != H3A_ABI_VERSION)
+        return fail(H3A_EINVAL, "%s: abi_version %d, library is %d", fn, a->abi_version, H3A_ABI_VERSION);
+    if (a->head_dim != 128) return fail(H3A_EUNSUPPORTED, "%s: head_dim must be 128, got %lld", fn, (long long)a->head_dim);
+    if (a->num_sections < 1 || a->num_sections > H3A_PROJ_MAX_SECTIONS)
+        return fail(H3A_EINVAL, "%s: num_sections must be in [1, %d], got %d", fn, H3A_PROJ_MAX_SECTIONS, a->num_sections);
+    if (a->m < 0 || a->k <= 0) return fail(H3A_EINVAL, "%s: bad extents (m=%lld k=%lld)", fn, (long long)a->m, (long long)a->k);
+    const int64_t step = h3a::proj_gemm_k_multiple();
+    if (a->k % step != 0)
+        return fail(H3A_EUNSUPPORTED, "%s: k must be a multiple of %lld, got %lld", fn, (long long)step, (long long)a->k);
+    const int64_t R = a->rotary_dim;
+    bool any_norm = false;
+    for (int i = 0; i < a->num_sections; ++i) any_norm |= a->sections[i].mode == H3A_PROJ_QKNORM_ROPE;
+    if (any_norm && (R < 0 || R > 128 || R % 2 != 0))
+        return fail(H3A_EINVAL,
+                    "fused qknorm+rope requires an even rotary dimension no wider than the head, got rotary_dim=%lld, "
+                    "head_dim=128",
+                    (long long)R);
+    if (!a->x || !aligned16(a->x)) return fail(H3A_EINVAL, "%s: x must be a 16-byte aligned device pointer", fn);
+    if (a->x_stride < a->k || a->x_stride % 8 != 0)
+        return fail(H3A_EINVAL, "%s: x_stride must be a multiple of 8 elements and at least k", fn);
+    const int64_t tile = h3a::proj_gemm_tile();
+    // Every buffer resource spans one tile of rows from its base.
+    const int64_t span_limit = ((int64_t)1 << 32) - 1;
+    if ((tile - 1) * a->x_stride * 2 + a->k * 2 > span_limit)
+        return fail(H3A_EUNSUPPORTED, "%s: x_stride too large", fn);
+    if (a->m >= ((int64_t)1 << 31)) return fail(H3A_EUNSUPPORTED, "%s: m too large", fn);
+    h3a::ProjGemmParams p{};
+    p.x = a->x;
+    p.x_rs = a->x_stride * 2;
+    p.m = (int32_t)a->m;
+    p.k = (int32_t)a->k;
+    p.n_sections = a->num_sections;
+    int64_t n_tiles = 0;
+    for (int i = 0; i < a->num_sections; ++i) {
+        const h3a_proj_section& s = a->sections[i];
+        if (s.mode != H3A_PROJ_PLAIN && s.mode != H3A_PROJ_QKNORM_ROPE)
+            return fail(H3A_EINVAL, "%s: section %d: unknown mode %d", fn, i, s.mode);
+        if (s.n <= 0 || s.n % 128 != 0 || s.n >= ((int64_t)1 << 30))
+            return fail(H3A_EUNSUPPORTED, "%s: section %d: n must be a positive multiple of 128, got %lld", fn, i,
+                        (long long)s.n);
+        if (!s.weight || !s.y || !aligned16(s.weight) || !aligned16(s.y))
+            return fail(H3A_EINVAL, "%s: section %d: weight and y must be 16-byte aligned device pointers", fn, i);
+        if (s.weight_stride < a->k || s.weight_stride % 8 != 0 || s.y_stride < s.n || s.y_stride % 8 != 0)
+            return fail(H3A_EINVAL, "%s: section %d: strides must be multiples of 8 elements covering the row", fn, i);
+        if ((tile - 1) * s.weight_stride * 2 + a->k * 2 > span_limit)
+            return fail(H3A_EUNSUPPORTED, "%s: section %d: weight_stride too large", fn, i);
+        if (s.bias && ((uintptr_t)s.bias & 7u) != 0)
+            return fail(H3A_EINVAL, "%s: section %d: bias must be 8-byte aligned", fn, i);
+        if (s.mode == H3A_PROJ_QKNORM_ROPE) {
+            if (!s.norm_weight || ((uintptr_t)s.norm_weight & 7u) != 0)
+                return fail(H3A_EINVAL, "%s: section %d: norm_weight must be an 8-byte aligned device pointer", fn, i);
+            if (!(s.eps >= 0.f) || !isfinite(s.eps)) return fail(H3A_EINVAL, "%s: section %d: bad eps", fn, i);
+        }
+        h3a::ProjSection& d = p.sec[i];
+        d.w = s.weight;
+        d.bias = s.bias;
+        d.norm_w = s.norm_weight;
+        d.y = s.y;
+        d.w_rs = s.weight_stride * 2;
+        d.y_rs = s.y_stride * 2;
+        d.n = (int32_t)s.n;
+        d.tiles = (int32_t)((s.n + tile - 1) / tile);
+        d.mode = s.mode;
+        d.eps = s.eps;
+        n_tiles += d.tiles;
+    }
+    if (any_norm && R % 32 != 0)
+        return fail(H3A_EUNSUPPORTED,
+                    "%s: rotary_dim %lld: the fused epilogue takes multiples of 32 (0, 32, 64, 96, 128); use a plain "
+                    "projection and h3a_qknorm_rope",
+                    fn, (long long)R);
+    if (any_norm && R > 0 && a->rotate_half_tables != 1)
+        return fail(H3A_EUNSUPPORTED,
+                    "%s: the fused epilogue reads rotate-half tables (columns c and c + rotary_dim/2 equal, "
+                    "rotate_half_tables = 1); use a plain projection and h3a_qknorm_rope",
+                    fn);
+    if (any_norm && R > 0) {
+        if (!a->cos || !a->sin) return fail(H3A_EINVAL, "%s: NULL cos/sin table", fn);
+        if (a->seqlen <= 0 || a->seqlen >= ((int64_t)1 << 31)) return fail(H3A_EINVAL, "%s: seqlen must be in [1, 2^31)", fn);
+        if (a->table_stride < R) return fail(H3A_EINVAL, "%s: table_stride < rotary_dim", fn);
+        if (!aligned16(a->cos) || !aligned16(a->sin) || a->table_stride % 4 != 0)
+            return fail(H3A_EINVAL, "%s: cos/sin must be 16-byte aligned with table_stride a multiple of 4", fn);
+        p.cos = a->cos;
+        p.sin = a->sin;
+        p.table_stride = a->table_stride;
+        p.rotary_dim = (int32_t)R;
+        p.seqlen = (int32_t)a->seqlen;
+    } else {
+        p.rotary_dim = 0;
+        p.seqlen = 1;
+    }
+    if (a->m == 0) return H3A_OK;
+    p.m_tiles = (int32_t)((a->m + tile - 1) / tile);
+    p.n_tiles = (int32_t)n_tiles;
+    if ((int64_t)p.m_tiles * n_tiles >= ((int64_t)1 << 31)) return fail(H3A_EUNSUPPORTED, "%s: grid too large", fn);
+    hipError_t e = h3a::launch_proj_gemm(p, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(H3A_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
+    return H3A_OK;
+}
+
 }  // extern "C"

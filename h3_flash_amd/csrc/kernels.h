@@ -219,4 +219,37 @@ struct AttnMergeParams {
 };
 hipError_t launch_attn_merge(const AttnMergeParams& p, hipStream_t stream);
 
+// Projection GEMM with the q/k norm + RoPE epilogue. Byte strides. Each
+// section is a range of output features with its own weight rows, bias,
+// output and epilogue (mode 0: plain, 1: RMSNorm over each 128-feature head,
+// norm weight, RoPE).
+struct ProjSection {
+    const void* w;       // bf16 (n, k), w_rs bytes per row
+    const void* bias;    // bf16 (n,) or NULL
+    const void* norm_w;  // bf16 (128,) (mode 1)
+    void* y;             // bf16 (m, n), y_rs bytes per row
+    int64_t w_rs, y_rs;
+    int32_t n;           // features, a multiple of 128
+    int32_t tiles;       // ceil(n / 256)
+    int32_t mode;
+    float eps;
+};
+constexpr int kProjMaxSections = 3;
+struct ProjGemmParams {
+    const void* x;  // bf16 (m, k), x_rs bytes per row
+    int64_t x_rs;
+    int32_t m, k;   // k a multiple of proj_gemm_k_multiple()
+    int32_t m_tiles, n_tiles;  // n_tiles = sum of the sections' tiles
+    int32_t n_sections;
+    ProjSection sec[kProjMaxSections];
+    const float* cos;  // fp32 (seqlen, table_stride) rotate-half tables (mode-1 sections with rotary_dim > 0)
+    const float* sin;
+    int64_t table_stride;
+    int32_t rotary_dim;
+    int32_t seqlen;  // token m uses table row m % seqlen
+};
+int proj_gemm_tile();
+int proj_gemm_k_multiple();  // k must be a multiple of this
+hipError_t launch_proj_gemm(const ProjGemmParams& p, hipStream_t stream);
+
 }  // namespace h3a

@@ -59,7 +59,7 @@ extern "C" {
 /* The library is built with hidden visibility; only these symbols export. */
 #define H3A_API __attribute__((visibility("default")))
 
-#define H3A_ABI_VERSION 3
+#define H3A_ABI_VERSION 4
 
 #define H3A_OK 0
 #define H3A_EINVAL (-1)       /* invalid argument (shape, stride, pointer) */
@@ -420,6 +420,77 @@ typedef struct h3a_attn_merge_args {
 } h3a_attn_merge_args;
 
 H3A_API int h3a_attn_merge(const h3a_attn_merge_args *args, void *stream);
+
+/*
+ * Projection GEMM of an H3 attention block with the q/k prologue as its
+ * epilogue. For every token row m of x and output feature f of a section,
+ *   acc = sum_k x[m, k] * weight[f, k] + bias[f]        (fp32 accumulation)
+ * and then per section mode:
+ *   H3A_PROJ_PLAIN:        y[m, f] = bf16(acc)
+ *   H3A_PROJ_QKNORM_ROPE:  per head (128 consecutive features) of token m,
+ *     n = acc * rsqrt(sum(acc^2) / 128 + eps) * norm_weight[f mod 128], then
+ *     rotate-half RoPE over the head's first rotary_dim features with table
+ *     row s = m mod seqlen:
+ *       y[c] = n[c] cos[s,c] - n[c+R/2] sin[s,c]   (c < R/2)
+ *       y[c] = n[c] cos[s,c] + n[c-R/2] sin[s,c]   (R/2 <= c < R)
+ *       y[c] = n[c]                                (c >= R)
+ *     stored once as bf16 (rotary_dim 0: the norm alone).
+ * This is the reference's projection step followed by its fused q/k norm +
+ * RoPE without the intermediate bf16 rounding of the projection output:
+ *   attn.to_qkv(hidden_states).chunk(3) or to_q / to_k / to_v
+ *     (src/h3_flash/runtime/attention/dense_fa4.py:123-128,
+ *      src/h3_flash/runtime/kernels/transformer.py:146-152),
+ *   norm_q / norm_k and _apply_rotary_emb, or fused_qknorm_rope
+ *     (dense_fa4.py:132-140, transformer.py:155-173, fusions.py:268-293),
+ *   and attn.to_out[0] (dense_fa4.py:169) as one PLAIN section.
+ * x: bf16 (m, k) with row stride x_stride elements; weight: bf16 (n, k) rows
+ * (the nn.Linear layout); y: bf16 (m, n) with row stride y_stride. Up to three
+ * sections (q, k, v of one fused or three separate weights) share x and run in
+ * one launch. head_dim must be 128; k a positive multiple of 128; each n a
+ * positive multiple of 128; x, weight and y 16-byte aligned with strides that
+ * are multiples of 8 elements; bias and norm_weight (bf16) 8-byte aligned;
+ * rotary_dim a multiple of 32 (other widths: a PLAIN projection followed by
+ * h3a_qknorm_rope); cos / sin fp32 (seqlen rows of table_stride floats),
+ * 16-byte aligned, table_stride a multiple of 4. No workspace; nothing is
+ * allocated.
+ */
+#define H3A_PROJ_PLAIN 0
+#define H3A_PROJ_QKNORM_ROPE 1
+#define H3A_PROJ_MAX_SECTIONS 3
+
+typedef struct h3a_proj_section {
+    const void *weight;      /* bf16 (n, k) */
+    int64_t weight_stride;   /* elements between weight rows */
+    int64_t n;               /* output features */
+    const void *bias;        /* bf16 (n,) or NULL */
+    void *y;                 /* bf16 (m, n) */
+    int64_t y_stride;        /* elements between y rows */
+    int32_t mode;            /* H3A_PROJ_PLAIN or H3A_PROJ_QKNORM_ROPE */
+    const void *norm_weight; /* bf16 (head_dim,), H3A_PROJ_QKNORM_ROPE only */
+    float eps;
+} h3a_proj_section;
+
+typedef struct h3a_proj_args {
+    int32_t abi_version;
+    const void *x;      /* bf16 (m, k) */
+    int64_t x_stride;   /* elements between x rows */
+    int64_t m;
+    int64_t k;
+    int64_t head_dim;   /* 128 */
+    int32_t num_sections;
+    h3a_proj_section sections[H3A_PROJ_MAX_SECTIONS];
+    const float *cos;   /* fp32 (seqlen, table_stride), or NULL when rotary_dim is 0 */
+    const float *sin;
+    int64_t table_stride;
+    int64_t rotary_dim; /* 0, 32, 64, 96 or 128 */
+    int64_t seqlen;     /* table rows; token row m uses row m % seqlen */
+    int32_t rotate_half_tables; /* must be 1 when rotary_dim > 0: the caller guarantees
+                                   cos[:, c] == cos[:, c + R/2] and sin[:, c] == sin[:, c + R/2]
+                                   (the cat(theta, theta) form of rotate-half RoPE tables);
+                                   only the first R/2 columns are read */
+} h3a_proj_args;
+
+H3A_API int h3a_proj_gemm(const h3a_proj_args *args, void *stream);
 
 /* Message of the last failed call on this thread ("" if none). */
 H3A_API const char *h3a_last_error(void);

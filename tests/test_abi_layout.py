@@ -26,6 +26,8 @@ STRUCTS = {
     "h3a_residual_gate_rmsnorm_modulate_args": _ext.ResidualGateRmsnormModulateArgs,
     "h3a_swiglu_args": _ext.SwigluArgs,
     "h3a_attn_merge_args": _ext.AttnMergeArgs,
+    "h3a_proj_section": _ext.ProjSection,
+    "h3a_proj_args": _ext.ProjArgs,
 }
 
 

@@ -41,6 +41,7 @@ def test_header_declares_the_expected_entry_points():
         "h3a_last_error",
         "h3a_merge_heads",
         "h3a_pack_qkv",
+        "h3a_proj_gemm",
         "h3a_qknorm_rope",
         "h3a_qknorm_rope_pack",
         "h3a_residual_gate_rmsnorm_modulate",
@@ -56,7 +57,7 @@ def test_library_exports_every_declared_function(lib):
 
 
 def test_abi_version(lib):
-    assert lib.h3a_abi_version() == _ext.ABI_VERSION == 3
+    assert lib.h3a_abi_version() == _ext.ABI_VERSION == 4
 
 
 def _attn_args(**overrides):
