@@ -228,19 +228,20 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
 
     // bias, then RMSNorm over the head (sum of squares in-lane, then over
     // lanes l ^ 16 and l ^ 32) and the norm weight.
-    auto normed = [&](int b, float (&v)[8][4]) __attribute__((always_inline)) {
-        // Four partial sums (over e), added at the end: short dependency
-        // chains for a lone wave.
-        float s4[4] = {0.f, 0.f, 0.f, 0.f};
+    auto normed = [&](int b, float (&v)[8][4], auto norm_c) __attribute__((always_inline)) {
 #pragma unroll
         for (int a = 0; a < 8; ++a)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v[a][e] = acc[a][b][e] + bias[a][e];
-                s4[e] += v[a][e] * v[a][e];
-            }
-        float ss = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-        if (norm) {
+            for (int e = 0; e < 4; ++e) v[a][e] = acc[a][b][e] + bias[a][e];
+        if constexpr (decltype(norm_c)::value) {
+            // Four partial sums (over e), added at the end: short dependency
+            // chains for a lone wave.
+            float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) s4[e] += v[a][e] * v[a][e];
+            float ss = (s4[0] + s4[1]) + (s4[2] + s4[3]);
             auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
             ss = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
             const f32x2 h = halves(ss);
@@ -256,7 +257,7 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
     // R a multiple of 32: every RoPE partner (c +- R/2, R/2 a multiple of 16)
     // is held by the same lane, feature block a pairing with a +- R/32, and
     // both use the table columns of block a mod R/32.
-    auto in_lane = [&](auto rh_c) __attribute__((always_inline)) {
+    auto in_lane = [&](auto rh_c, auto norm_c) __attribute__((always_inline)) {
         constexpr int rh = decltype(rh_c)::value, ra = 2 * rh;  // half of the rotated blocks, all of them
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
@@ -269,7 +270,7 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
                 if (b + 1 < 8) load_tables(b + 1);
             }
             float v[8][4];
-            normed(b, v);
+            normed(b, v, norm_c);
             const int r = 16 * b + j16;
 #pragma unroll
             for (int a = 0; a < 8; ++a) {
@@ -292,12 +293,17 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
             }
         }
     };
-    switch (R) {
-        case 0: in_lane(std::integral_constant<int, 0>{}); break;
-        case 32: in_lane(std::integral_constant<int, 1>{}); break;
-        case 64: in_lane(std::integral_constant<int, 2>{}); break;
-        case 96: in_lane(std::integral_constant<int, 3>{}); break;
-        default: in_lane(std::integral_constant<int, 4>{}); break;  // 128 (the caller admits multiples of 32)
+    using Y = std::true_type;
+    if (!norm) {
+        in_lane(std::integral_constant<int, 0>{}, std::false_type{});
+    } else {
+        switch (R) {
+            case 0: in_lane(std::integral_constant<int, 0>{}, Y{}); break;
+            case 32: in_lane(std::integral_constant<int, 1>{}, Y{}); break;
+            case 64: in_lane(std::integral_constant<int, 2>{}, Y{}); break;
+            case 96: in_lane(std::integral_constant<int, 3>{}, Y{}); break;
+            default: in_lane(std::integral_constant<int, 4>{}, Y{}); break;  // 128 (the caller admits multiples of 32)
+        }
     }
     if (!active) return;
     // Lane l moves bytes 16*(l & 15) .. +16 of token row 4*it + (l >> 4) (the
