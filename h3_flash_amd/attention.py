@@ -34,6 +34,7 @@ import torch
 
 from . import _ext
 from .audit import gate_qknorm_rope
+from .projection import out_projection, qkv_projection
 from .prologue import fused_qk_norm_rope
 
 __all__ = [
@@ -290,9 +291,13 @@ class DenseMiniMaxH3Processor:
     _attention_backend = None
     _parallel_config = None
 
-    def __init__(self, *, kernel: Callable[..., Any] | None = None) -> None:
+    def __init__(self, *, kernel: Callable[..., Any] | None = None, fuse_projections: bool = False) -> None:
         self.kernel = load_kernel() if kernel is None else kernel
         self.calls = 0
+        # True: q/k/v come from one h3a_proj_gemm launch with the q/k RMSNorm
+        # + RoPE in its epilogue, and to_out[0] runs on it too (modules or
+        # inputs outside what it takes keep the separate steps).
+        self.fuse_projections = fuse_projections
         # Set by install_dense_hip on the first module: the install record,
         # whose "gate" receives the fused prologue's error on the first call
         # (transformer.py:174-190).
@@ -311,6 +316,26 @@ class DenseMiniMaxH3Processor:
             raise RuntimeError(
                 "dense HIP attention runs one GPU's head shard; context parallelism is not installed"
             )
+        fused = qkv_projection(attn, hidden_states, rotary_emb) if self.fuse_projections else None
+        if fused is not None:
+            query, key, value = fused
+            if self._runtime is not None and "qknorm_partial_rope" not in self._runtime["gate"]:
+                self._runtime["gate"]["qknorm_partial_rope"] = gate_qknorm_rope(attn, hidden_states, query, *rotary_emb)
+        else:
+            query, key, value = self._projections(attn, hidden_states, rotary_emb)
+        output = self.kernel(query, key, value, causal=False)
+        if isinstance(output, tuple):
+            output = output[0]
+        self.calls += 1
+        output = output.flatten(2, 3).type_as(query)
+        projected = out_projection(attn.to_out[0], output) if self.fuse_projections else None
+        output = attn.to_out[0](output) if projected is None else projected
+        return attn.to_out[1](output)
+
+    def _projections(self, attn: Any, hidden_states: torch.Tensor, rotary_emb: Any):
+        """The separate steps: projections, then the fused q/k prologue (or the
+        module's norms without RoPE)."""
+
         if attn.fused_projections:
             query, key, value = attn.to_qkv(hidden_states).chunk(3, dim=-1)
         else:
@@ -334,16 +359,12 @@ class DenseMiniMaxH3Processor:
             query, key = fused_qk_norm_rope(query, key, nq[0], nk[0], cos, sin, nq[1], nk[1])
             if self._runtime is not None and "qknorm_partial_rope" not in self._runtime["gate"]:
                 self._runtime["gate"]["qknorm_partial_rope"] = gate_qknorm_rope(attn, hidden_states, query, cos, sin)
-        output = self.kernel(query, key, value, causal=False)
-        if isinstance(output, tuple):
-            output = output[0]
-        self.calls += 1
-        output = output.flatten(2, 3).type_as(query)
-        output = attn.to_out[0](output)
-        return attn.to_out[1](output)
+        return query, key, value
 
 
-def install_dense_hip(transformer: Any, attention_class: type | None = None) -> dict[str, Any]:
+def install_dense_hip(
+    transformer: Any, attention_class: type | None = None, *, fuse_projections: bool = False
+) -> dict[str, Any]:
     """Install one shared HIP kernel on every H3 attention module.
 
     Mirrors ``install_dense_fa4`` (dense_fa4.py:173-194). Modules are matched
@@ -366,7 +387,7 @@ def install_dense_hip(transformer: Any, attention_class: type | None = None) -> 
             else type(module).__name__ == "MiniMaxH3Attention"
         )
         if matched:
-            processor = DenseMiniMaxH3Processor(kernel=kernel)
+            processor = DenseMiniMaxH3Processor(kernel=kernel, fuse_projections=fuse_projections)
             processor._parallel_config = getattr(transformer, "_parallel_config", None)
             module.set_processor(processor)
             processors.append(processor)

@@ -409,3 +409,72 @@ def test_attn_merge_null_part_and_empty(lib):
     a.part_lse_stride[:] = (-8, 8)
     assert lib.h3a_attn_merge(ctypes.byref(a), None) == _ext.H3A_EINVAL
     assert "LSE strides must be non-negative" in _ext.last_error(lib)
+
+
+def _proj_args(n_sections=3, **overrides):
+    a = _ext.ProjArgs()
+    a.abi_version = _ext.ABI_VERSION
+    a.x = 1 << 20
+    a.x_stride, a.m, a.k, a.head_dim = 256, 300, 256, 128
+    a.num_sections = n_sections
+    for i in range(n_sections):
+        d = a.sections[i]
+        d.weight, d.weight_stride, d.n = (1 << 24) + i * (1 << 20), 256, 256
+        d.y, d.y_stride = (1 << 28) + i * 512, 768
+        d.mode = _ext.H3A_PROJ_QKNORM_ROPE if i < 2 else _ext.H3A_PROJ_PLAIN
+        d.norm_weight, d.eps = 1 << 22, 1e-6
+    a.cos, a.sin, a.table_stride, a.rotary_dim, a.seqlen = 1 << 21, (1 << 21) + (1 << 19), 128, 128, 300
+    a.rotate_half_tables = 1
+    for k, v in overrides.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize(
+    "overrides, code, message",
+    [
+        ({"abi_version": 3}, _ext.H3A_EINVAL, "abi_version"),
+        ({"head_dim": 64}, _ext.H3A_EUNSUPPORTED, "head_dim must be 128"),
+        ({"num_sections": 0}, _ext.H3A_EINVAL, "num_sections"),
+        ({"num_sections": 4}, _ext.H3A_EINVAL, "num_sections"),
+        ({"k": 200, "x_stride": 256}, _ext.H3A_EUNSUPPORTED, "multiple of 128"),
+        ({"rotary_dim": 45}, _ext.H3A_EINVAL, "even rotary dimension no wider than the head"),
+        ({"rotary_dim": 130}, _ext.H3A_EINVAL, "even rotary dimension no wider than the head"),
+        ({"rotary_dim": 48}, _ext.H3A_EUNSUPPORTED, "multiples of 32"),
+        ({"rotate_half_tables": 0}, _ext.H3A_EUNSUPPORTED, "rotate-half"),
+        ({"x": (1 << 20) + 8}, _ext.H3A_EINVAL, "x must be a 16-byte aligned"),
+        ({"x_stride": 252}, _ext.H3A_EINVAL, "x_stride"),
+        ({"cos": None}, _ext.H3A_EINVAL, "NULL cos/sin"),
+        ({"table_stride": 64}, _ext.H3A_EINVAL, "table_stride"),
+        ({"sin": (1 << 21) + 8}, _ext.H3A_EINVAL, "16-byte aligned"),
+        ({"seqlen": 0}, _ext.H3A_EINVAL, "seqlen"),
+        ({"m": -1}, _ext.H3A_EINVAL, "extents"),
+    ],
+)
+@host_only
+def test_proj_gemm_validation(lib, overrides, code, message):
+    a = _proj_args(**overrides)
+    assert lib.h3a_proj_gemm(ctypes.byref(a), None) == code
+    assert message in _ext.last_error(lib)
+
+
+@host_only
+def test_proj_gemm_section_validation(lib):
+    for field, value, message in [
+        ("n", 200, "multiple of 128"),
+        ("weight", (1 << 24) + 4, "16-byte aligned"),
+        ("weight_stride", 100, "strides"),
+        ("y_stride", 100, "strides"),
+        ("mode", 7, "unknown mode"),
+        ("bias", (1 << 23) + 4, "bias must be 8-byte aligned"),
+        ("norm_weight", None, "norm_weight"),
+    ]:
+        a = _proj_args()
+        setattr(a.sections[0], field, value)
+        assert lib.h3a_proj_gemm(ctypes.byref(a), None) != _ext.H3A_OK, field
+        assert message in _ext.last_error(lib), (field, _ext.last_error(lib))
+    # plain sections only: no tables needed, rotary_dim and the table flag ignored
+    a = _proj_args(n_sections=1, rotary_dim=48, rotate_half_tables=0, cos=None, sin=None, m=0)
+    a.sections[0].mode = _ext.H3A_PROJ_PLAIN
+    assert lib.h3a_proj_gemm(ctypes.byref(a), None) == _ext.H3A_OK
+    assert lib.h3a_proj_gemm(None, None) == _ext.H3A_EINVAL
