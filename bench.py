@@ -324,11 +324,17 @@ def block_rates(torch, heads: int = 40, head_dim: int = 128, grid=(32, 30, 52)) 
         o = functional.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
         return attn.to_out[0](o.transpose(1, 2).flatten(2, 3))
 
+    fused_processor = DenseMiniMaxH3Processor(fuse_projections=True)
+
     def ours():
         return processor(attn, x, (cos, sin))
 
+    def ours_fused():
+        return fused_processor(attn, x, (cos, sin))
+
     with torch.no_grad():
         ours_ms = _time_ms(torch, ours, reps=5)
+        fused_ms = _time_ms(torch, ours_fused, reps=5)
         eager_ms = _time_ms(torch, eager, reps=3)
     attn_flop = 4.0 * S * S * head_dim * heads
     proj_flop = 2.0 * S * (heads * head_dim) ** 2 * 4
@@ -336,11 +342,93 @@ def block_rates(torch, heads: int = 40, head_dim: int = 128, grid=(32, 30, 52)) 
         "workload": f"one H3 attention block: B=1 S={S} heads={heads} head_dim={head_dim} hidden={heads * head_dim}, "
         "random-init weights, bf16",
         "hip_processor_ms": ours_ms,
+        "hip_processor_fused_projections_ms": fused_ms,
         "eager_torch_sdpa_ms": eager_ms,
         "speedup": eager_ms / ours_ms,
         "flop_per_block": attn_flop + proj_flop,
         "hip_processor_TFLOP_s": (attn_flop + proj_flop) / (ours_ms * 1e-3) / 1e12,
     }
+
+
+def projection_rates(torch, hidden: int = 5120) -> dict:
+    """The block's projections on one GPU: h3a_proj_gemm (q, k, v in one
+    launch with the q/k RMSNorm + RoPE epilogue; the out-projection as one
+    plain section) against hipBLASLt (torch's linear) followed by the HIP
+    q/k prologue, at one 8-way Ulysses rank's tokens (6,240) and at the full
+    49,920 tokens of 40 heads."""
+
+    from torch.nn import functional
+
+    from h3_flash_amd.projection import Section, proj_gemm
+    from h3_flash_amd.prologue import fused_qk_norm_rope
+    from h3_flash_amd.rope import rope_3d_tables
+
+    dev = torch.device("cuda:0")
+    heads = hidden // 128
+    g = torch.Generator(device=dev).manual_seed(31)
+    w = (torch.randn((3 * hidden, hidden), device=dev, generator=g) / hidden**0.5).to(torch.bfloat16)
+    b = (torch.randn((3 * hidden,), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    wo = (torch.randn((hidden, hidden), device=dev, generator=g) / hidden**0.5).to(torch.bfloat16)
+    bo = (torch.randn((hidden,), device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    nw = (1 + 0.1 * torch.randn((2, 128), device=dev, generator=g)).to(torch.bfloat16)
+    out = {"hidden": hidden, "heads": heads, "peak_TFLOP_s": PEAK_BF16_TFLOPS}
+    for name, grid in (("rank_480p_8way", (4, 30, 52)), ("full_480p_40_heads", (32, 30, 52))):
+        S = grid[0] * grid[1] * grid[2]
+        cos, sin = (t.to(dev) for t in rope_3d_tables(grid))
+        x = torch.randn((S, hidden), device=dev, generator=g).to(torch.bfloat16)
+        y = torch.empty((S, 3 * hidden), device=dev, dtype=torch.bfloat16)
+        yo = torch.empty((S, hidden), device=dev, dtype=torch.bfloat16)
+        n = hidden
+        secs = [
+            Section(w[:n], y[:, :n], b[:n], nw[0], 1e-6),
+            Section(w[n : 2 * n], y[:, n : 2 * n], b[n : 2 * n], nw[1], 1e-6),
+            Section(w[2 * n :], y[:, 2 * n :], b[2 * n :]),
+        ]
+
+        def fused():
+            proj_gemm(x, secs, cos, sin, S)
+
+        def separate():
+            q, k, v = (functional.linear(x, w[i * n : (i + 1) * n], b[i * n : (i + 1) * n]) for i in range(3))
+            shape = (1, S, heads, 128)
+            return fused_qk_norm_rope(q.view(shape), k.view(shape), nw[0], nw[1], cos, sin, 1e-6, 1e-6), v
+
+        def one_gemm():
+            qkv = functional.linear(x, w, b).view(1, S, 3 * heads, 128)
+            q, k, v = qkv.chunk(3, dim=2)
+            return fused_qk_norm_rope(q, k, nw[0], nw[1], cos, sin, 1e-6, 1e-6), v
+
+        def prologue_only():
+            q = y[:, :n].view(1, S, heads, 128)
+            return fused_qk_norm_rope(q, q, nw[0], nw[1], cos, sin, 1e-6, 1e-6)
+
+        def out_ours():
+            proj_gemm(x, [Section(wo, yo, bo)])
+
+        def out_torch():
+            return functional.linear(x, wo, bo)
+
+        with torch.no_grad():
+            t = {k: _time_ms(torch, f, reps=10) for k, f in (
+                ("h3a_proj_gemm_qkv_fused_epilogue", fused),
+                ("hipblaslt_3_linears_then_hip_prologue", separate),
+                ("hipblaslt_one_linear_then_hip_prologue", one_gemm),
+                ("hip_prologue_alone", prologue_only),
+                ("h3a_proj_gemm_out_projection", out_ours),
+                ("hipblaslt_out_projection", out_torch),
+            )}
+        qkv_flop, out_flop = 2.0 * S * hidden * 3 * hidden, 2.0 * S * hidden * hidden
+        out[name] = {
+            "tokens": S,
+            "ms": t,
+            "qkv_TFLOP_s_fused": qkv_flop / (t["h3a_proj_gemm_qkv_fused_epilogue"] * 1e-3) / 1e12,
+            "out_TFLOP_s": {k: out_flop / (t[k] * 1e-3) / 1e12 for k in ("h3a_proj_gemm_out_projection", "hipblaslt_out_projection")},
+            "fused_vs_best_separate": min(t["hipblaslt_3_linears_then_hip_prologue"], t["hipblaslt_one_linear_then_hip_prologue"])
+            / t["h3a_proj_gemm_qkv_fused_epilogue"],
+            "out_projection_vs_hipblaslt": t["hipblaslt_out_projection"] / t["h3a_proj_gemm_out_projection"],
+        }
+        del x, y, yo
+    return out
 
 
 def read_pmc_traffic() -> dict | None:
@@ -606,6 +694,7 @@ def main(argv=None) -> int:
     result["fusions"] = None if args.no_relayout else fusion_rates(torch)
     result["cp_merge"] = None if args.no_relayout else merge_rates(torch)
     result["block"] = None if args.no_block else block_rates(torch)
+    result["projections"] = None if args.no_block else projection_rates(torch)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, q, k, v, w.heads, args.cpu_rows, args.cpu_repeats)
     else:
