@@ -147,8 +147,10 @@ static_assert(kPSmem <= 160 * 1024, "LDS of one workgroup");
 
 // Epilogue of one tile: bias, then per section mode the plain value or the
 // RMSNorm + norm weight + RoPE of each 128-feature head, rounded once to
-// bf16 into the wave's LDS rows, which then go out as 16-byte stores (4
-// token rows of 256 bytes per instruction). Every wave of the workgroup
+// bf16. Without RoPE the values go straight out as 16-byte stores (lane
+// pairs trade halves so each lane holds 8 consecutive features); with it
+// they go into the wave's LDS rows first, which then go out as 16-byte
+// stores (4 token rows of 256 bytes per instruction). Every wave of the workgroup
 // calls it (RoPE sections have barriers); `active` is false for the wave
 // whose head lies past the section. The RoPE tables are in the rotate-half
 // form (columns c and c + R/2 equal), so only their first R/2 columns are
@@ -272,6 +274,31 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
             float v[8][4];
             normed(b, v, norm_c);
             const int r = 16 * b + j16;
+            if constexpr (ra == 0) {
+                // No tables to wait for: stores go out directly. Lanes l and
+                // l ^ 16 (feature groups q, q ^ 1) trade one of two feature
+                // blocks 2j, 2j+1, so that the even lane holds 8 consecutive
+                // features of block 2j and the odd lane of block 2j+1: one
+                // 16-byte store each, 64 contiguous bytes per token.
+                const int m = m_head + r;
+                const bool even = ((lane >> 4) & 1) == 0;
+                char* const yr = (char*)sec.y + (int64_t)m * sec.y_rs + (int64_t)f_head * 2;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t p0x = pack_bf16x2(v[2 * j][0], v[2 * j][1]), p0y = pack_bf16x2(v[2 * j][2], v[2 * j][3]);
+                    const uint32_t p1x = pack_bf16x2(v[2 * j + 1][0], v[2 * j + 1][1]);
+                    const uint32_t p1y = pack_bf16x2(v[2 * j + 1][2], v[2 * j + 1][3]);
+                    const uint32_t sx = even ? p1x : p0x, sy = even ? p1y : p0y;
+                    auto rx = __builtin_amdgcn_permlane16_swap(sx, sx, false, false);
+                    auto ry = __builtin_amdgcn_permlane16_swap(sy, sy, false, false);
+                    const uint32_t gx = even ? rx[1] : rx[0], gy = even ? ry[1] : ry[0];  // the partner's
+                    const i32x4 w = even ? i32x4{(int)p0x, (int)p0y, (int)gx, (int)gy}
+                                         : i32x4{(int)gx, (int)gy, (int)p1x, (int)p1y};
+                    const int f = 32 * j + (even ? 0 : 16) + 4 * ((lane >> 4) & 2);
+                    if (active && m < p.m) *(i32x4*)(yr + f * 2) = w;
+                }
+                continue;
+            }
 #pragma unroll
             for (int a = 0; a < 8; ++a) {
                 float y[4];
@@ -305,7 +332,7 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
             default: in_lane(std::integral_constant<int, 4>{}, Y{}); break;  // 128 (the caller admits multiples of 32)
         }
     }
-    if (!active) return;
+    if (!active || !rope) return;  // without tables the stores went out directly
     // Lane l moves bytes 16*(l & 15) .. +16 of token row 4*it + (l >> 4) (the
     // wave's LDS ops are ordered, so its own writes are visible here).
     char* const yb = (char*)sec.y + (int64_t)f_head * 2 + j16 * 16;
