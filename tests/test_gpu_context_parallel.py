@@ -67,6 +67,21 @@ def test_merge_head_dims(D, n):
     assert (l.cpu()[fin] - rl[fin]).abs().max().item() <= 1e-5
 
 
+@pytest.mark.parametrize("D", [8, 128])
+def test_merge_batched(D):
+    # workgroups take 16 tokens of one head (D = 8: four heads' groups); the
+    # sequence is not a multiple of 16, so each batch's last chunk is partial
+    g = torch.Generator().manual_seed(D)
+    B, S, H, n = 3, 37, 2, 4
+    outs = [torch.randn((B, S, H, D), generator=g).to(torch.bfloat16) for _ in range(n)]
+    lses = [torch.randn((B, H, S), generator=g) * 4 for _ in range(n)]
+    lses[2][1, 0, 5:20] = float("-inf")
+    o, l = merge_attention([x.to(DEV) for x in outs], [x.to(DEV) for x in lses])
+    ro, rl = merge_reference(outs, lses)
+    assert_parity(o, ro.to(torch.bfloat16), f"batched D={D}")
+    assert (l.cpu() - rl).abs().max().item() <= 1e-5
+
+
 def test_merge_more_than_sixteen_parts_and_in_place():
     outs, lses = _partials(21, S=64, seed=3)
     ro, rl = merge_reference(outs, lses)
