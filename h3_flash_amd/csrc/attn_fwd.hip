@@ -145,10 +145,20 @@ __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory
 // instead of two transpose reads. The K rows of every 16-key group are then
 // taken in the order that swaps bits 2 and 3 of the key index (keyperm), so
 // that the eight keys a lane holds in P^T are consecutive.
-template <bool kWide, bool kVT>
-__device__ __forceinline__ void attn_tile(const AttnParams& p, int tile, int chunk, int chunks, int slot,
-                                          bool graded = false) {
+// The launch arguments as the tail loop reads them: where they lie (the
+// kernel-argument segment, through the scalar cache).
+using KernArgs = const __attribute__((address_space(4))) AttnParams;
+
+// The tile's LDS: one array however many copies of attn_tile a kernel holds.
+__device__ __forceinline__ char* attn_lds() {
     __shared__ __attribute__((aligned(1024))) char smem[kLdsBytes];
+    return smem;
+}
+
+template <bool kWide, bool kVT, typename Params>
+__device__ __forceinline__ void attn_tile(Params& p, int tile, int chunk, int chunks, int slot,
+                                          bool graded = false) {
+    char* const smem = attn_lds();
     // V stages 0..3 first, then K stages 0..3: with a per-lane base in a VGPR
     // every fragment read offset then fits the 16-bit ds_read immediate.
     char* const vst = smem;
@@ -774,7 +784,16 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
             chunks = p.split_n;
             slot = piece;
         }
-        attn_tile<kWide, kVT>(p, tile, chunk, chunks, slot, !planned);
+        // The launch arguments are read afresh for each piece (an opaque zero
+        // offset keeps the compiler from hoisting the loads), from the
+        // kernel-argument segment through the scalar cache, rather than held
+        // in scalar registers across the loop: the piece's own addressing
+        // needs those registers (spills of scalar registers to VGPR lanes
+        // fell from 84 to 28 in the dense kernel).
+        int zero;
+        asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+        KernArgs* pk = (KernArgs*)((const __attribute__((address_space(4))) char*)&p + zero);
+        attn_tile<kWide, kVT>(*pk, tile, chunk, chunks, slot, !planned);
     }
 }
 
