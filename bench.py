@@ -692,6 +692,8 @@ def main(argv=None) -> int:
     result["reference_harness"] = None if args.no_sdpa else reference_harness(torch, q, k, v, out, w.segments, ms_per_step, flops)
     result["relayout"] = None if args.no_relayout else relayout_rates(torch)
     result["fusions"] = None if args.no_relayout else fusion_rates(torch)
+    # the whole 480p/5s sequence on one GPU (no Ulysses split), 40 heads
+    result["fusions_full_sequence"] = None if args.no_relayout else fusion_rates(torch, rows=49920, hidden=5120)
     result["cp_merge"] = None if args.no_relayout else merge_rates(torch)
     result["block"] = None if args.no_block else block_rates(torch)
     result["projections"] = None if args.no_block else projection_rates(torch)
