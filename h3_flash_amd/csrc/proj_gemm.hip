@@ -127,21 +127,12 @@ struct TileSrc {
     int32_t w_rs;
 };
 
-// Epilogue LDS use:
-//  - the output rows, over the stage memory once the K loop is done: per
-//    wave 128 tokens x 256 bytes, the 8-byte chunk c of row r at
-//    c ^ (r mod 32), so that the 16 rows of a quarter-wave's writes fall in
-//    distinct bank pairs;
-//  - RoPE tables, past the stage memory: per pair of waves with the same
-//    tokens (wm), two buffers of one token block's cos and sin rows, the
-//    first R/2 <= 64 columns of each (16 rows x 256 bytes per table; the
-//    16-byte chunk c of row j at c ^ j, so the 16 rows of a quarter-wave's
-//    reads fall in 16 distinct bank groups).
+// Epilogue LDS use: the output rows of RoPE sections, over the stage memory
+// once the K loop is done: per wave 128 tokens x 256 bytes, the 8-byte chunk
+// c of row r at c ^ (r mod 32), so that the 16 rows of a quarter-wave's
+// writes fall in distinct bank pairs.
 constexpr int kPOutWave = 128 * 256;
-constexpr int kPTabRow = 256;
-constexpr int kPTabBuf = 2 * 16 * kPTabRow;  // cos then sin rows of one token block
-constexpr int kPTabBase = kPLds;
-constexpr int kPSmem = kPTabBase + 2 * 2 * kPTabBuf;
+constexpr int kPSmem = kPLds;
 static_assert(kPWaves * kPOutWave <= kPLds, "output rows fit the stage memory");
 static_assert(kPSmem <= 160 * 1024, "LDS of one workgroup");
 
@@ -150,15 +141,12 @@ static_assert(kPSmem <= 160 * 1024, "LDS of one workgroup");
 // bf16. Without RoPE the values go straight out as 16-byte stores (lane
 // pairs trade halves so each lane holds 8 consecutive features); with it
 // they go into the wave's LDS rows first, which then go out as 16-byte
-// stores (4 token rows of 256 bytes per instruction). Every wave of the workgroup
-// calls it (RoPE sections have barriers); `active` is false for the wave
-// whose head lies past the section. The RoPE tables are in the rotate-half
-// form (columns c and c + R/2 equal), so only their first R/2 columns are
-// read: the two waves of a token range copy one token block's rows HBM ->
-// LDS (cos by one, sin by the other, whole rows per load) while the previous
-// block is computed. The epilogue's loads all complete before its first
-// store, so no wait for a load is also a wait for stores in flight (one
-// counter covers both).
+// stores (4 token rows of 256 bytes per instruction). The waves work
+// independently (no barrier); `active` is false for the wave whose head
+// lies past the section. The RoPE tables are in the rotate-half form
+// (columns c and c + R/2 equal), so only their first R/2 columns are read,
+// each lane loading its own token's values into registers one token block
+// ahead.
 __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoord& tc, const f32x4 (&acc)[8][8],
                                          int wave, int wn, int wm, int lane, char* smem) {
     // Opaque here, so that no lane-derived value of the epilogue is hoisted
@@ -179,37 +167,22 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
     const int seqlen = p.seqlen;
     const int m_head = tc.m0 + wm * 128;  // first token of the wave
 
-    // Table copy of token block b into buffer b & 1 of the wave pair: this
-    // wave copies cos (wn = 0) or sin (wn = 1); load k moves rows 4k..4k+3,
-    // lane L writing chunk L & 15 of row 4k + (L >> 4), which holds the row's
-    // chunk (L & 15) ^ row. Rows past the tables (and columns past the table
-    // on its last row) are outside the resource's records and load as zeros.
+    // RoPE tables straight into registers: for token block b the lane loads,
+    // from its token's rows (wrapped per sequence), the first-half columns
+    // 16*ta + fl .. +3 of cos and sin for each rotated block pair ta. The
+    // loads of block b+1 are issued before block b is computed; the RoPE
+    // path issues no stores until its rows are complete, so each wait is for
+    // the tables alone (one counter covers loads and stores).
     const uint32_t tab_bytes = (uint32_t)((int64_t)seqlen * p.table_stride * 4);
-    const i32x4 rtab = make_rsrc_words(wn ? (const void*)p.sin : (const void*)p.cos, tab_bytes);
-    char* const tabs = smem + kPTabBase + wm * 2 * kPTabBuf;
-    const uint32_t lds_tabs = (uint32_t)(uintptr_t)(const lds_char*)tabs;
+    const auto rcos = make_rsrc(p.cos, tab_bytes);
+    const auto rsin = make_rsrc(p.sin, tab_bytes);
     const uint32_t row_bytes = (uint32_t)(p.table_stride * 4);
-    auto load_tables = [&](int b) __attribute__((always_inline)) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int row = 4 * k + (lane >> 4);
-            int s = m_head + 16 * b + row;
-            s = s < seqlen ? s : s % seqlen;
-            const uint32_t voff = (uint32_t)s * row_bytes + ((((lane & 15) ^ row) & 15) << 4);
-            const uint32_t m0v = lds_tabs + (b & 1) * kPTabBuf + wn * 16 * kPTabRow + 4 * k * kPTabRow;
-            asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                         :
-                         : "s"(m0v), "v"(voff), "s"(rtab)
-                         : "memory");
-        }
-    };
-    // The lane's table values of (first-half) feature block a, token block b.
-    auto tab = [&](int b, int sin_, int a) __attribute__((always_inline)) {
-        const lds_char* const t = (const lds_char*)tabs + (b & 1) * kPTabBuf + sin_ * 16 * kPTabRow + j16 * kPTabRow;
-        return *(const lds_f32x4*)(t + ((((4 * a + (lane >> 4)) ^ j16) & 15) << 4));
+    auto tab_offset = [&](int b) __attribute__((always_inline)) {
+        int s = m_head + 16 * b + j16;
+        s = s < seqlen ? s : s % seqlen;
+        return (uint32_t)s * row_bytes + (uint32_t)fl * 4u;
     };
     const bool rope = R > 0;
-    if (rope) load_tables(0);
 
     // Bias and norm weight of the lane's features (bf16, widened to fp32).
     const bool has_bias = sec.bias != nullptr;
@@ -261,15 +234,21 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
     // both use the table columns of block a mod R/32.
     auto in_lane = [&](auto rh_c, auto norm_c) __attribute__((always_inline)) {
         constexpr int rh = decltype(rh_c)::value, ra = 2 * rh;  // half of the rotated blocks, all of them
+        constexpr int nt = rh > 0 ? rh : 1;
+        f32x4 tcv[2][nt], tsv[2][nt];
+        auto load_regs = [&](int b) __attribute__((always_inline)) {
+            const uint32_t o = tab_offset(b);
+#pragma unroll
+            for (int ta = 0; ta < rh; ++ta) {
+                tcv[b & 1][ta] = __builtin_bit_cast(f32x4, buf_load16(rcos, o + 64u * ta));
+                tsv[b & 1][ta] = __builtin_bit_cast(f32x4, buf_load16(rsin, o + 64u * ta));
+            }
+        };
+        if constexpr (ra > 0) load_regs(0);
 #pragma unroll
         for (int b = 0; b < 8; ++b) {
             if constexpr (ra > 0) {
-                // This wave's copy of block b has landed; after the barrier
-                // the pair's whole copy has, and every wave is past block
-                // b-1, whose buffer block b+1 now takes.
-                wait_vm_lgkm<0>();
-                barrier();
-                if (b + 1 < 8) load_tables(b + 1);
+                if (b + 1 < 8) load_regs(b + 1);
             }
             float v[8][4];
             normed(b, v, norm_c);
@@ -305,7 +284,7 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
                 if (a < ra) {
                     const int pa = a < rh ? a + rh : a - rh;
                     const int ta = a < rh ? a : a - rh;
-                    const f32x4 cw = tab(b, 0, ta), sw = tab(b, 1, ta);
+                    const f32x4 cw = tcv[b & 1][ta], sw = tsv[b & 1][ta];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const float rot = a < rh ? -v[pa][e] : v[pa][e];
