@@ -70,6 +70,8 @@ def _inputs(rows, hidden, n_table=9, table_dtype=torch.bfloat16, seed=0):
         # one wave per row (bf16 tables, 512 columns per vector step): one
         # full vector, the widest (11 per lane), one column step past it
         (6, 512, torch.bfloat16, torch.bfloat16, torch.int32),
+        (5, 8, torch.bfloat16, torch.bfloat16, torch.int64),  # one vector, on lane 0 only
+        (3, 24, torch.bfloat16, torch.float32, torch.int32),
         (10, 5632, torch.bfloat16, torch.float32, torch.int64),
         (7, 5640, torch.bfloat16, torch.bfloat16, torch.int32),
     ],
@@ -93,6 +95,7 @@ def test_rmsnorm_modulate(rows, hidden, table_dtype, wdtype, idtype):
         (7, 2056, torch.float32, torch.float32),
         (3, 16384, torch.bfloat16, torch.float32),
         (6, 4104, torch.bfloat16, torch.float32),  # one wave per row, last vector on one lane
+        (9, 16, torch.bfloat16, torch.bfloat16),
         (5, 5632, torch.bfloat16, torch.bfloat16),
     ],
 )
