@@ -763,6 +763,8 @@ int h3a_proj_gemm(const h3a_proj_args* a, void* stream) {
         if (!a->cos || !a->sin) return fail(H3A_EINVAL, "%s: NULL cos/sin table", fn);
         if (a->seqlen <= 0 || a->seqlen >= ((int64_t)1 << 31)) return fail(H3A_EINVAL, "%s: seqlen must be in [1, 2^31)", fn);
         if (a->table_stride < R) return fail(H3A_EINVAL, "%s: table_stride < rotary_dim", fn);
+        if (a->seqlen * a->table_stride * 4 > span_limit)
+            return fail(H3A_EUNSUPPORTED, "%s: cos/sin tables must span less than 2^32 bytes", fn);
         if (!aligned16(a->cos) || !aligned16(a->sin) || a->table_stride % 4 != 0)
             return fail(H3A_EINVAL, "%s: cos/sin must be 16-byte aligned with table_stride a multiple of 4", fn);
         p.cos = a->cos;

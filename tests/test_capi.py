@@ -448,6 +448,7 @@ def _proj_args(n_sections=3, **overrides):
         ({"table_stride": 64}, _ext.H3A_EINVAL, "table_stride"),
         ({"sin": (1 << 21) + 8}, _ext.H3A_EINVAL, "16-byte aligned"),
         ({"seqlen": 0}, _ext.H3A_EINVAL, "seqlen"),
+        ({"seqlen": 1 << 23}, _ext.H3A_EUNSUPPORTED, "less than 2^32 bytes"),  # 8M rows x 512 bytes
         ({"m": -1}, _ext.H3A_EINVAL, "extents"),
     ],
 )
