@@ -729,6 +729,9 @@ int h3a_proj_gemm(const h3a_proj_args* a, void* stream) {
             return fail(H3A_EINVAL, "%s: section %d: strides must be multiples of 8 elements covering the row", fn, i);
         if ((tile - 1) * s.weight_stride * 2 + a->k * 2 > span_limit)
             return fail(H3A_EUNSUPPORTED, "%s: section %d: weight_stride too large", fn, i);
+        // A wave's output resource spans half a tile of token rows.
+        if ((tile / 2 - 1) * s.y_stride * 2 + 256 > span_limit)
+            return fail(H3A_EUNSUPPORTED, "%s: section %d: y_stride too large", fn, i);
         if (s.bias && ((uintptr_t)s.bias & 7u) != 0)
             return fail(H3A_EINVAL, "%s: section %d: bias must be 8-byte aligned", fn, i);
         if (s.mode == H3A_PROJ_QKNORM_ROPE) {

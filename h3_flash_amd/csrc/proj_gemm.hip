@@ -229,6 +229,15 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
         }
     };
     lds_char* const orow = (lds_char*)smem + wave * kPOutWave;
+    // Direct stores (sections without RoPE) go through a resource over this
+    // wave's 128 token rows of its head: rows past the launch's tokens lie
+    // outside its records and are dropped, and a wave whose head is past the
+    // section gets no records at all, so no store needs a branch. f_pair:
+    // byte offset of the lane's 8 features within a 32-feature group.
+    const int rows_valid = active ? max(0, min(128, p.m - m_head)) : 0;
+    const auto yout = make_rsrc((const char*)sec.y + (int64_t)m_head * sec.y_rs + (int64_t)f_safe * 2,
+                                rows_valid > 0 ? (uint32_t)((rows_valid - 1) * sec.y_rs + 256) : 0u);
+    const uint32_t f_pair = (uint32_t)((((lane >> 4) & 1) ? 16 : 0) + 4 * ((lane >> 4) & 2)) * 2u;
     // R a multiple of 32: every RoPE partner (c +- R/2, R/2 a multiple of 16)
     // is held by the same lane, feature block a pairing with a +- R/32, and
     // both use the table columns of block a mod R/32.
@@ -256,25 +265,21 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
             if constexpr (ra == 0) {
                 // No tables to wait for: stores go out directly. Lanes l and
                 // l ^ 16 (feature groups q, q ^ 1) trade one of two feature
-                // blocks 2j, 2j+1, so that the even lane holds 8 consecutive
-                // features of block 2j and the odd lane of block 2j+1: one
-                // 16-byte store each, 64 contiguous bytes per token.
-                const int m = m_head + r;
-                const bool even = ((lane >> 4) & 1) == 0;
-                char* const yr = (char*)sec.y + (int64_t)m * sec.y_rs + (int64_t)f_head * 2;
+                // blocks 2j, 2j+1 (permlane16_swap exchanges the first
+                // operand of the odd lane with the second of the even one),
+                // so that the even lane holds 8 consecutive features of
+                // block 2j and the odd lane of block 2j+1: one 16-byte store
+                // each, 64 contiguous bytes per token.
+                const uint32_t row_off = (uint32_t)r * (uint32_t)sec.y_rs;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const uint32_t p0x = pack_bf16x2(v[2 * j][0], v[2 * j][1]), p0y = pack_bf16x2(v[2 * j][2], v[2 * j][3]);
                     const uint32_t p1x = pack_bf16x2(v[2 * j + 1][0], v[2 * j + 1][1]);
                     const uint32_t p1y = pack_bf16x2(v[2 * j + 1][2], v[2 * j + 1][3]);
-                    const uint32_t sx = even ? p1x : p0x, sy = even ? p1y : p0y;
-                    auto rx = __builtin_amdgcn_permlane16_swap(sx, sx, false, false);
-                    auto ry = __builtin_amdgcn_permlane16_swap(sy, sy, false, false);
-                    const uint32_t gx = even ? rx[1] : rx[0], gy = even ? ry[1] : ry[0];  // the partner's
-                    const i32x4 w = even ? i32x4{(int)p0x, (int)p0y, (int)gx, (int)gy}
-                                         : i32x4{(int)gx, (int)gy, (int)p1x, (int)p1y};
-                    const int f = 32 * j + (even ? 0 : 16) + 4 * ((lane >> 4) & 2);
-                    if (active && m < p.m) *(i32x4*)(yr + f * 2) = w;
+                    const auto sx = __builtin_amdgcn_permlane16_swap(p0x, p1x, false, false);
+                    const auto sy = __builtin_amdgcn_permlane16_swap(p0y, p1y, false, false);
+                    const i32x4 w{(int)sx[0], (int)sy[0], (int)sx[1], (int)sy[1]};
+                    __builtin_amdgcn_raw_buffer_store_b128(w, yout, (int)(row_off + (uint32_t)(64 * j) + f_pair), 0, 0);
                 }
                 continue;
             }

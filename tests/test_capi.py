@@ -469,6 +469,7 @@ def test_proj_gemm_section_validation(lib):
         ("mode", 7, "unknown mode"),
         ("bias", (1 << 23) + 4, "bias must be 8-byte aligned"),
         ("norm_weight", None, "norm_weight"),
+        ("y_stride", 1 << 25, "y_stride too large"),  # 127 rows of 64 MiB pass 2^32 bytes
     ]:
         a = _proj_args()
         setattr(a.sections[0], field, value)
