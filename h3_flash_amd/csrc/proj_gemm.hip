@@ -234,9 +234,16 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
     // outside its records and are dropped, and a wave whose head is past the
     // section gets no records at all, so no store needs a branch. f_pair:
     // byte offset of the lane's 8 features within a 32-feature group.
+    // (Base and size go through readfirstlane: uniform, but the compiler
+    // would otherwise keep the resource in VGPRs and wrap every store in a
+    // waterfall loop.)
     const int rows_valid = active ? max(0, min(128, p.m - m_head)) : 0;
-    const auto yout = make_rsrc((const char*)sec.y + (int64_t)m_head * sec.y_rs + (int64_t)f_safe * 2,
-                                rows_valid > 0 ? (uint32_t)((rows_valid - 1) * sec.y_rs + 256) : 0u);
+    const uint64_t ybase = (uint64_t)(uintptr_t)((const char*)sec.y + (int64_t)m_head * sec.y_rs + (int64_t)f_safe * 2);
+    const uint32_t ybytes = rows_valid > 0 ? (uint32_t)((rows_valid - 1) * sec.y_rs + 256) : 0u;
+    const auto yout = make_rsrc(
+        (const void*)(uintptr_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(ybase >> 32)) << 32) |
+                                 (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)ybase)),
+        (uint32_t)__builtin_amdgcn_readfirstlane((int)ybytes));
     const uint32_t f_pair = (uint32_t)((((lane >> 4) & 1) ? 16 : 0) + 4 * ((lane >> 4) & 2)) * 2u;
     // R a multiple of 32: every RoPE partner (c +- R/2, R/2 a multiple of 16)
     // is held by the same lane, feature block a pairing with a +- R/32, and
