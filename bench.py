@@ -495,7 +495,7 @@ def reference_harness(torch, q, k, v, out, segments, hip_ms: float, flops: float
             native = sdpa()
             torch.cuda.synchronize()
             ms = _time_ms(torch, sdpa, reps=reps)
-    except RuntimeError as exc:  # no fused SDPA backend for this shape on this build
+    except RuntimeError as exc:  # torch has no fused SDPA backend for this shape
         return {"torch_sdpa": None, "error": str(exc)[:200]}
     ref = native.float()
     delta = ref - out.float()
@@ -549,7 +549,7 @@ def main(argv=None) -> int:
     args = parse_args(argv)
     if args.gpus != 1:
         print(
-            "bench.py measures one MI355X: the attention runs one GPU's head shard and this build "
+            "bench.py measures one MI355X: the attention runs one GPU's head shard and the library "
             f"launches no collectives; --gpus {args.gpus} is not supported (use --gpus 1).",
             file=sys.stderr,
         )

@@ -63,7 +63,7 @@ extern "C" {
 
 #define H3A_OK 0
 #define H3A_EINVAL (-1)       /* invalid argument (shape, stride, pointer) */
-#define H3A_EUNSUPPORTED (-2) /* valid request this build does not implement */
+#define H3A_EUNSUPPORTED (-2) /* valid request the library does not implement */
 #define H3A_ELAUNCH (-3)      /* the HIP launch itself failed */
 
 /* dtype codes: norm weights and modulation tables (bf16 / fp32), table indices (int32 / int64) */

@@ -1,7 +1,7 @@
 """CPU oracle of the dense H3 attention path — TEST INFRASTRUCTURE ONLY.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline
-leg may import this package, and only as the checker. The product
+leg may import this package, and only to check results against it. The product
 (``h3_flash_amd``) never calls it and has no CPU fallback.
 
 Modules, each citing the reference lines it restates:
