@@ -187,17 +187,19 @@ __global__ __launch_bounds__(kThreads) void modulate_kernel(ModulateParams p) {
 }
 
 // Wave path (C % 8 == 0, C <= 64 * 8 * kRowVecMax, 16-byte aligned rows):
-// one wave per row, four rows per workgroup, no barrier. Each wave issues its
-// row's loads (x, residual) and then every weight and table vector it will
-// need, all before the first wait, and holds its outputs until the end: on
-// gfx9 one counter covers loads and stores, so a store issued ahead of a load
-// would make that load's wait also wait for the store. The row index, and so
-// the row bases and the modulation-table row, are wave-uniform (scalar
-// registers; lanes add 32-bit offsets). Measured against the one-row-per-
-// workgroup kernel below on 49,920 x 5,120 rows: 5.4 -> 6.0 TB/s
-// (rmsnorm_modulate) and 5.3 -> 5.9 TB/s (residual variant), level at 6,240
-// rows. Used for bf16 tables up to 11 vectors per lane (C <= 5,632), where
-// it keeps two or more waves per SIMD; the block kernel takes the rest.
+// one wave per row, four rows per workgroup, which share the weight row
+// through LDS (one barrier). Each wave issues its row's loads (x, or
+// residual and branch, and the gate row) and then every scale and shift
+// vector it will need, all before the first wait, and holds its outputs
+// until the end: on gfx9 one counter covers loads and stores, so a store
+// issued ahead of a load would make that load's wait also wait for the
+// store. The row index, and so the row bases and the modulation-table row,
+// are wave-uniform (scalar registers; lanes add 32-bit offsets). Measured
+// against the one-row-per-workgroup kernel below on 49,920 x 5,120 rows:
+// 5.4 -> 6.0 TB/s (rmsnorm_modulate) and 5.3 -> 6.1 TB/s (residual
+// variant); at 6,240 rows within 2%. Used for bf16 tables up to 11 vectors
+// per lane (C <= 5,632), where it keeps two waves per SIMD; the block kernel
+// takes the rest.
 constexpr int kRowVecMax = 11;
 
 __device__ __forceinline__ float wave_sum(float v) {
@@ -230,8 +232,9 @@ template <int NV, bool kResidual, bool kTabF32, bool kWF32>
 __global__ __launch_bounds__(kThreads) void modulate_row_kernel(ModulateParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-    const int64_t row = (int64_t)blockIdx.x * kWaves + wave;  // uniform: row bases and t in scalar registers
-    if (row >= p.rows) return;
+    const int64_t row_id = (int64_t)blockIdx.x * kWaves + wave;  // uniform: row bases and t in scalar registers
+    const bool live = row_id < p.rows;
+    const int64_t row = live ? row_id : p.rows - 1;  // a wave past the rows loads the last one, stores nothing
     const int C = p.cols;
     // Vectors 0 .. NV-2 of a lane lie inside the row (NV = ceil(C / 512));
     // the last one, where it does not, is loaded from the row's last vector
@@ -257,8 +260,27 @@ __global__ __launch_bounds__(kThreads) void modulate_row_kernel(ModulateParams p
     const char* const wrow = (const char*)p.weight;
     const char* const scrow = (const char*)p.scale + t * p.scale_stride * tb_sz;
     const char* const shrow = (const char*)p.shift + t * p.shift_stride * tb_sz;
+    // The weight row, shared by the workgroup's four rows, goes through LDS:
+    // vector i (columns 8i .. 8i+7, the last clamped into the row) at wl[i].
+    constexpr int kWv = NV * 64, kWl = kWF32 ? 2 : 1;
+    __shared__ i32x4 wl[kWv * kWl];
+    {
+        constexpr int kIt = (kWv + kThreads - 1) / kThreads;
+        Raw8<kWF32> wv[kIt];
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int i = min((int)threadIdx.x + it * kThreads, kWv - 1);
+            wv[it] = fetch8o<kWF32>(wrow, (uint32_t)min(i * 8, C - 8) * 2u);
+        }
+#pragma unroll
+        for (int it = 0; it < kIt; ++it) {
+            const int i = min((int)threadIdx.x + it * kThreads, kWv - 1);
+            wl[i * kWl] = wv[it].a;
+            if constexpr (kWF32) wl[i * kWl + 1] = wv[it].b;
+        }
+    }
     auto tabs = [&](int k) __attribute__((always_inline)) {
-        return RowTabs<kTabF32, kWF32>{fetch8o<kWF32>(wrow, off[k]), fetch8o<kTabF32>(scrow, off[k]), fetch8o<kTabF32>(shrow, off[k])};
+        return RowTabs<kTabF32, kWF32>{Raw8<kWF32>{}, fetch8o<kTabF32>(scrow, off[k]), fetch8o<kTabF32>(shrow, off[k])};
     };
     float ss = 0.f;
     float h[kResidual ? NV : 1][8];
@@ -276,7 +298,7 @@ __global__ __launch_bounds__(kThreads) void modulate_row_kernel(ModulateParams p
             unpack8(rx[k], b);
 #pragma unroll
             for (int e = 0; e < 8; ++e) h[k][e] = r[e] + gv[e] * b[e];
-            if (k < NV - 1 || last) {
+            if (live && (k < NV - 1 || last)) {
                 __builtin_nontemporal_store(pack8(h[k]), (i32x4*)(hr + off[k]));
 #pragma unroll
                 for (int e = 0; e < 8; ++e) ss += h[k][e] * h[k][e];
@@ -301,6 +323,8 @@ __global__ __launch_bounds__(kThreads) void modulate_row_kernel(ModulateParams p
         for (int k = 0; k < NV; ++k) asm volatile("" : "+v"(rx[k]));
     }
     const float r = rsqrtf(wave_sum(ss) / (float)C + p.eps);
+    __syncthreads();  // the weight row is in LDS
+    if (!live) return;
     i32x4 ov[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -311,7 +335,12 @@ __global__ __launch_bounds__(kThreads) void modulate_row_kernel(ModulateParams p
         } else {
             unpack8(rx[k], v);
         }
-        unpack_raw8<kWF32>(tb[k].w, wv);
+        {
+            Raw8<kWF32> w;
+            w.a = wl[(lane + 64 * k) * kWl];
+            if constexpr (kWF32) w.b = wl[(lane + 64 * k) * kWl + 1];
+            unpack_raw8<kWF32>(w, wv);
+        }
         unpack_raw8<kTabF32>(tb[k].sc, scv);
         unpack_raw8<kTabF32>(tb[k].sh, shv);
 #pragma unroll
