@@ -195,7 +195,7 @@ __global__ __launch_bounds__(kThreads) void modulate_kernel(ModulateParams p) {
 // issued ahead of a load would make that load's wait also wait for the
 // store. The row index, and so the row bases and the modulation-table row,
 // are wave-uniform (scalar registers; lanes add 32-bit offsets). Measured
-// against the one-row-per-workgroup kernel below on 49,920 x 5,120 rows:
+// against the one-row-per-workgroup kernel above on 49,920 x 5,120 rows:
 // 5.4 -> 6.0 TB/s (rmsnorm_modulate) and 5.3 -> 6.1 TB/s (residual
 // variant); at 6,240 rows within 2%. Used for bf16 tables up to 11 vectors
 // per lane (C <= 5,632), where it keeps two waves per SIMD; the block kernel
@@ -208,9 +208,8 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-template <bool kTabF32, bool kWF32>
+template <bool kTabF32>
 struct RowTabs {
-    Raw8<kWF32> w;
     Raw8<kTabF32> sc, sh;
 };
 
@@ -280,7 +279,7 @@ __global__ __launch_bounds__(kThreads) void modulate_row_kernel(ModulateParams p
         }
     }
     auto tabs = [&](int k) __attribute__((always_inline)) {
-        return RowTabs<kTabF32, kWF32>{Raw8<kWF32>{}, fetch8o<kTabF32>(scrow, off[k]), fetch8o<kTabF32>(shrow, off[k])};
+        return RowTabs<kTabF32>{fetch8o<kTabF32>(scrow, off[k]), fetch8o<kTabF32>(shrow, off[k])};
     };
     float ss = 0.f;
     float h[kResidual ? NV : 1][8];
@@ -305,7 +304,7 @@ __global__ __launch_bounds__(kThreads) void modulate_row_kernel(ModulateParams p
             }
         }
     }
-    RowTabs<kTabF32, kWF32> tb[NV];
+    RowTabs<kTabF32> tb[NV];
 #pragma unroll
     for (int k = 0; k < NV; ++k) tb[k] = tabs(k);
     if constexpr (!kResidual) {
