@@ -247,6 +247,7 @@ struct ProjGemmParams {
     int64_t table_stride;
     int32_t rotary_dim;
     int32_t seqlen;  // token m uses table row m % seqlen
+    int32_t stage_plain;  // 1: sections without RoPE stage their rows in LDS like the RoPE sections
 };
 int proj_gemm_tile();
 int proj_gemm_k_multiple();  // k must be a multiple of this

@@ -183,6 +183,7 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
         return (uint32_t)s * row_bytes + (uint32_t)fl * 4u;
     };
     const bool rope = R > 0;
+    const bool staged = rope || p.stage_plain != 0;  // rows go out through LDS
 
     // Bias and norm weight of the lane's features (bf16, widened to fp32).
     const bool has_bias = sec.bias != nullptr;
@@ -269,7 +270,7 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
             float v[8][4];
             normed(b, v, norm_c);
             const int r = 16 * b + j16;
-            if constexpr (ra == 0) {
+            if (ra == 0 && !staged) {
                 // No tables to wait for: stores go out directly. Lanes l and
                 // l ^ 16 (feature groups q, q ^ 1) trade one of two feature
                 // blocks 2j, 2j+1 (permlane16_swap exchanges the first
@@ -323,7 +324,7 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
             default: in_lane(std::integral_constant<int, 4>{}, Y{}); break;  // 128 (the caller admits multiples of 32)
         }
     }
-    if (!active || !rope) return;  // without tables the stores went out directly
+    if (!active || !staged) return;  // the rows went out directly
     // Lane l moves bytes 16*(l & 15) .. +16 of token row 4*it + (l >> 4) (the
     // wave's LDS ops are ordered, so its own writes are visible here).
     char* const yb = (char*)sec.y + (int64_t)f_head * 2 + j16 * 16;
@@ -335,8 +336,8 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
         const i32x2 hi = *(const __attribute__((address_space(3))) i32x2*)(src + ((((2 * j16 + 1) ^ r) & 31) << 3));
         const int m = m_head + r;
         // Non-temporal: whole 256-byte row pieces that no later tile reads
-        // (q and k of the 40-head block 3.5% faster; the plain sections'
-        // 64-byte pieces measured slower this way and keep ordinary stores).
+        // (q and k of the 40-head block 3.5% faster; the direct stores'
+        // 64-byte pieces measured slower this way and stay ordinary).
         if (m < p.m) __builtin_nontemporal_store(i32x4{lo.x, lo.y, hi.x, hi.y}, (i32x4*)(yb + (int64_t)m * sec.y_rs));
     }
 }
