@@ -294,7 +294,8 @@ class _H3Attention:
 
 def block_rates(torch, heads: int = 40, head_dim: int = 128, grid=(32, 30, 52)) -> dict:
     """One H3 attention block (projections, q/k RMSNorm + 3D RoPE, attention,
-    out-projection) through the HIP processor, against the reference's eager
+    out-projection) through the HIP processor (also with the projections
+    unfused, and with the out-projection fused too), against the reference's eager
     composition on the same GPU (dense_fa4.py:123-140,169-170 with torch SDPA
     as at packed_ulysses.py:202-209)."""
 
@@ -324,25 +325,29 @@ def block_rates(torch, heads: int = 40, head_dim: int = 128, grid=(32, 30, 52)) 
         o = functional.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
         return attn.to_out[0](o.transpose(1, 2).flatten(2, 3))
 
-    fused_processor = DenseMiniMaxH3Processor(fuse_projections=True)
+    unfused = DenseMiniMaxH3Processor(fuse_projections=False)
+    all_fused = DenseMiniMaxH3Processor(fuse_out_projection=True)
 
     def ours():
         return processor(attn, x, (cos, sin))
 
-    def ours_fused():
-        return fused_processor(attn, x, (cos, sin))
-
     with torch.no_grad():
         ours_ms = _time_ms(torch, ours, reps=5)
-        fused_ms = _time_ms(torch, ours_fused, reps=5)
+        unfused_ms = _time_ms(torch, lambda: unfused(attn, x, (cos, sin)), reps=5)
+        all_fused_ms = _time_ms(torch, lambda: all_fused(attn, x, (cos, sin)), reps=5)
         eager_ms = _time_ms(torch, eager, reps=3)
     attn_flop = 4.0 * S * S * head_dim * heads
     proj_flop = 2.0 * S * (heads * head_dim) ** 2 * 4
     return {
         "workload": f"one H3 attention block: B=1 S={S} heads={heads} head_dim={head_dim} hidden={heads * head_dim}, "
         "random-init weights, bf16",
+        # the processor as installed: q/k/v through the fused projection GEMM,
+        # the out-projection on hipBLASLt
         "hip_processor_ms": ours_ms,
-        "hip_processor_fused_projections_ms": fused_ms,
+        # every projection on hipBLASLt, then the HIP q/k prologue
+        "hip_processor_unfused_projections_ms": unfused_ms,
+        # the out-projection through the projection GEMM too
+        "hip_processor_fused_out_projection_ms": all_fused_ms,
         "eager_torch_sdpa_ms": eager_ms,
         "speedup": eager_ms / ours_ms,
         "flop_per_block": attn_flop + proj_flop,

@@ -291,13 +291,22 @@ class DenseMiniMaxH3Processor:
     _attention_backend = None
     _parallel_config = None
 
-    def __init__(self, *, kernel: Callable[..., Any] | None = None, fuse_projections: bool = False) -> None:
+    def __init__(
+        self,
+        *,
+        kernel: Callable[..., Any] | None = None,
+        fuse_projections: bool = True,
+        fuse_out_projection: bool = False,
+    ) -> None:
         self.kernel = load_kernel() if kernel is None else kernel
         self.calls = 0
-        # True: q/k/v come from one h3a_proj_gemm launch with the q/k RMSNorm
-        # + RoPE in its epilogue, and to_out[0] runs on it too (modules or
-        # inputs outside what it takes keep the separate steps).
+        # fuse_projections: q/k/v come from one h3a_proj_gemm launch with the
+        # q/k RMSNorm + RoPE in its epilogue (modules or inputs outside what
+        # it takes keep the separate steps). fuse_out_projection: to_out[0]
+        # runs on h3a_proj_gemm too; off by default, hipBLASLt's GEMM is 1-4%
+        # faster there and there is no epilogue to fold.
         self.fuse_projections = fuse_projections
+        self.fuse_out_projection = fuse_out_projection
         # Set by install_dense_hip on the first module: the install record,
         # whose "gate" receives the fused prologue's error on the first call
         # (transformer.py:174-190).
@@ -328,7 +337,7 @@ class DenseMiniMaxH3Processor:
             output = output[0]
         self.calls += 1
         output = output.flatten(2, 3).type_as(query)
-        projected = out_projection(attn.to_out[0], output) if self.fuse_projections else None
+        projected = out_projection(attn.to_out[0], output) if self.fuse_out_projection else None
         output = attn.to_out[0](output) if projected is None else projected
         return attn.to_out[1](output)
 
@@ -363,7 +372,11 @@ class DenseMiniMaxH3Processor:
 
 
 def install_dense_hip(
-    transformer: Any, attention_class: type | None = None, *, fuse_projections: bool = False
+    transformer: Any,
+    attention_class: type | None = None,
+    *,
+    fuse_projections: bool = True,
+    fuse_out_projection: bool = False,
 ) -> dict[str, Any]:
     """Install one shared HIP kernel on every H3 attention module.
 
@@ -387,7 +400,9 @@ def install_dense_hip(
             else type(module).__name__ == "MiniMaxH3Attention"
         )
         if matched:
-            processor = DenseMiniMaxH3Processor(kernel=kernel, fuse_projections=fuse_projections)
+            processor = DenseMiniMaxH3Processor(
+                kernel=kernel, fuse_projections=fuse_projections, fuse_out_projection=fuse_out_projection
+            )
             processor._parallel_config = getattr(transformer, "_parallel_config", None)
             module.set_processor(processor)
             processors.append(processor)

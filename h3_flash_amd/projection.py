@@ -146,9 +146,11 @@ def qkv_projection(
     module or inputs are outside what the fused launch takes (then nothing
     was launched)."""
 
-    H = attn.heads
     x = hidden_states
     if x.dim() != 3 or x.dtype != torch.bfloat16 or x.device.type != "cuda":
+        return None
+    H = getattr(attn, "heads", None)
+    if not isinstance(H, int):
         return None
     B, S, hidden = x.shape
     if hidden % 128 or not x.is_contiguous() or x.data_ptr() % 16 or B * S == 0:

@@ -200,17 +200,18 @@ def test_processor_with_fused_projections(fused):
     assert rotate_half_tables(cos, sin)
     assert qkv_projection(attn, x, (cos, sin)) is not None
     outs = {}
-    for fuse in (False, True):
-        processor = DenseMiniMaxH3Processor(fuse_projections=fuse)
+    for fuse, fuse_out in ((False, False), (True, False), (True, True)):
+        processor = DenseMiniMaxH3Processor(fuse_projections=fuse, fuse_out_projection=fuse_out)
         attn.set_processor(processor)
         with torch.no_grad():
-            outs[fuse] = attn(x, rotary_emb=(cos, sin)).float()
+            outs[fuse, fuse_out] = attn(x, rotary_emb=(cos, sin)).float()
         assert processor.calls == 1
     torch.cuda.synchronize()
-    # the two paths differ only by where q/k are rounded (once in the fused
+    # the paths differ only by where q/k are rounded (once in the fused
     # epilogue, twice in the separate steps) and the GEMMs' summation order
-    m = error_metrics(outs[True], outs[False])
-    assert m["finite"] and m["relative_l2"] < 1e-2 and m["cosine"] > 0.9999, m
+    for key in ((True, False), (True, True)):
+        m = error_metrics(outs[key], outs[False, False])
+        assert m["finite"] and m["relative_l2"] < 1e-2 and m["cosine"] > 0.9999, (key, m)
 
 
 def test_other_tables_keep_the_separate_steps():
