@@ -113,9 +113,9 @@ def test_3d_rope_tables_of_the_480p_grid():
     check_qkv(x, w, b, nwq, nwk, cos, sin, S, y)
 
 
-def test_many_tiles_per_persistent_workgroup():
-    # 17 token tiles x 60 feature tiles: several tiles per workgroup on any
-    # part with up to 1,020 CUs, each loading the next tile's data behind it
+def test_more_tiles_than_cus():
+    # 17 token tiles x 60 feature tiles: four rounds of workgroups over the
+    # XCDs' tile ranges, the last token tile ragged
     x, w, b, nwq, nwk = make(4096 + 96, 256, 40, 128, True, seed=7)
     cos, sin = tables(4192, 128, seed=1)
     y = run_qkv(x, w, b, nwq, nwk, cos, sin, 4192)
@@ -146,6 +146,25 @@ def test_plain_projection_matches_hipblaslt_linear():
     torch.cuda.synchronize()
     assert ours is not None and ours.shape == (1, 4136, 5120)
     d = (ours.view_as(ref).float() - ref.float()).abs()
+    ulp = 2.0 ** (torch.floor(torch.log2(ref.float().abs().clamp_min(1e-30))) - 7)
+    assert (d <= ulp).all(), float((d / ulp).max())
+    assert (d == 0).float().mean() > 0.99
+
+
+def test_wide_plain_rows_take_the_staged_stores():
+    # three plain sections writing 3 x 2,816 bf16 = 16.5 KiB rows: the rows
+    # go out through LDS like the RoPE sections' (narrower launches store
+    # from registers); every section within one ulp of hipBLASLt
+    g = torch.Generator(device=DEV).manual_seed(11)
+    m, k, n = 1000 + 40, 512, 2816
+    x = torch.randn((m, k), device=DEV, generator=g).to(torch.bfloat16)
+    w = (torch.randn((3 * n, k), device=DEV, generator=g) / k**0.5).to(torch.bfloat16)
+    b = (0.1 * torch.randn(3 * n, device=DEV, generator=g)).to(torch.bfloat16)
+    y = torch.empty((m, 3 * n), device=DEV, dtype=torch.bfloat16)
+    proj_gemm(x, [Section(w[i * n : (i + 1) * n], y[:, i * n : (i + 1) * n], b[i * n : (i + 1) * n]) for i in range(3)])
+    ref = torch.nn.functional.linear(x, w, b)
+    torch.cuda.synchronize()
+    d = (y.float() - ref.float()).abs()
     ulp = 2.0 ** (torch.floor(torch.log2(ref.float().abs().clamp_min(1e-30))) - 7)
     assert (d <= ulp).all(), float((d / ulp).max())
     assert (d == 0).float().mean() > 0.99
