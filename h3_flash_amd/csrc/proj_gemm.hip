@@ -138,10 +138,11 @@ static_assert(kPSmem <= 160 * 1024, "LDS of one workgroup");
 
 // Epilogue of one tile: bias, then per section mode the plain value or the
 // RMSNorm + norm weight + RoPE of each 128-feature head, rounded once to
-// bf16. Without RoPE the values go straight out as 16-byte stores (lane
-// pairs trade halves so each lane holds 8 consecutive features); with it
-// they go into the wave's LDS rows first, which then go out as 16-byte
-// stores (4 token rows of 256 bytes per instruction). The waves work
+// bf16. RoPE sections, and every section of a launch with RoPE sections or
+// 16 KiB output rows (p.stage_plain), put their values into the wave's LDS
+// rows first, which then go out as non-temporal 16-byte stores (4 token rows
+// of 256 bytes per instruction); the others store straight from registers
+// (lane pairs trade halves so each lane holds 8 consecutive features). The waves work
 // independently (no barrier); `active` is false for the wave whose head
 // lies past the section. The RoPE tables are in the rotate-half form
 // (columns c and c + R/2 equal), so only their first R/2 columns are read,
