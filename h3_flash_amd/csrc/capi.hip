@@ -107,8 +107,8 @@ int prepare_attn(const h3a_attn_args* a, h3a::AttnParams& p, bool* empty) {
     // rows of it must span less than 2^31 bytes.
     const int64_t window = h3a::attn_fwd_window_rows();
     for (int i = 0; i < 4; ++i) {
-        const int64_t span = window * st[i][1] * 2;
-        if (span >= kMaxWindow)
+        // window * stride * 2 >= kMaxWindow, without overflowing int64
+        if (st[i][1] >= (kMaxWindow + window * 2 - 1) / (window * 2))
             return fail(H3A_EUNSUPPORTED, "h3a_attn_fwd: %s row stride %lld elements is too large (%lld rows must span < 2^31 bytes)",
                         nm[i], (long long)st[i][1], (long long)window);
     }
@@ -706,7 +706,11 @@ int h3a_proj_gemm(const h3a_proj_args* a, void* stream) {
     const int64_t tile = h3a::proj_gemm_tile();
     // Every buffer resource spans one tile of rows from its base.
     const int64_t span_limit = ((int64_t)1 << 32) - 1;
-    if ((tile - 1) * a->x_stride * 2 + a->k * 2 > span_limit)
+    // rows * stride_elems * 2 + tail_bytes, checked without overflowing int64
+    auto spans = [&](int64_t rows, int64_t stride, int64_t tail) {
+        return stride <= (span_limit - tail) / 2 / rows;
+    };
+    if (a->k > span_limit / 2 || !spans(tile - 1, a->x_stride, a->k * 2))
         return fail(H3A_EUNSUPPORTED, "%s: x_stride too large", fn);
     if (a->m >= ((int64_t)1 << 31)) return fail(H3A_EUNSUPPORTED, "%s: m too large", fn);
     h3a::ProjGemmParams p{};
@@ -727,10 +731,10 @@ int h3a_proj_gemm(const h3a_proj_args* a, void* stream) {
             return fail(H3A_EINVAL, "%s: section %d: weight and y must be 16-byte aligned device pointers", fn, i);
         if (s.weight_stride < a->k || s.weight_stride % 8 != 0 || s.y_stride < s.n || s.y_stride % 8 != 0)
             return fail(H3A_EINVAL, "%s: section %d: strides must be multiples of 8 elements covering the row", fn, i);
-        if ((tile - 1) * s.weight_stride * 2 + a->k * 2 > span_limit)
+        if (!spans(tile - 1, s.weight_stride, a->k * 2))
             return fail(H3A_EUNSUPPORTED, "%s: section %d: weight_stride too large", fn, i);
         // A wave's output resource spans half a tile of token rows.
-        if ((tile / 2 - 1) * s.y_stride * 2 + 256 > span_limit)
+        if (!spans(tile / 2 - 1, s.y_stride, 256))
             return fail(H3A_EUNSUPPORTED, "%s: section %d: y_stride too large", fn, i);
         if (s.bias && ((uintptr_t)s.bias & 7u) != 0)
             return fail(H3A_EINVAL, "%s: section %d: bias must be 8-byte aligned", fn, i);
@@ -766,7 +770,7 @@ int h3a_proj_gemm(const h3a_proj_args* a, void* stream) {
         if (!a->cos || !a->sin) return fail(H3A_EINVAL, "%s: NULL cos/sin table", fn);
         if (a->seqlen <= 0 || a->seqlen >= ((int64_t)1 << 31)) return fail(H3A_EINVAL, "%s: seqlen must be in [1, 2^31)", fn);
         if (a->table_stride < R) return fail(H3A_EINVAL, "%s: table_stride < rotary_dim", fn);
-        if (a->seqlen * a->table_stride * 4 > span_limit)
+        if (a->table_stride > span_limit / 4 / a->seqlen)
             return fail(H3A_EUNSUPPORTED, "%s: cos/sin tables must span less than 2^32 bytes", fn);
         if (!aligned16(a->cos) || !aligned16(a->sin) || a->table_stride % 4 != 0)
             return fail(H3A_EINVAL, "%s: cos/sin must be 16-byte aligned with table_stride a multiple of 4", fn);

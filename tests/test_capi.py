@@ -91,6 +91,8 @@ def _attn_args(**overrides):
         ({"cu_seqlens_q": 1 << 20, "cu_seqlens_k": 1 << 20, "num_segments": 1, "max_seqlen_q": 99},
          _ext.H3A_EINVAL, "max_seqlen_q"),
         ({"q_stride": (ctypes.c_int64 * 3)(1 << 25, 1 << 21, 128)}, _ext.H3A_EUNSUPPORTED, "row stride"),
+        # a row stride whose window span would overflow a 64-bit product
+        ({"k_stride": (ctypes.c_int64 * 3)(1 << 62, 1 << 61, 128)}, _ext.H3A_EUNSUPPORTED, "row stride"),
         ({"lse": (1 << 20) + 2}, _ext.H3A_EINVAL, "lse must be 4-byte aligned"),
         ({"lse": 1 << 20, "lse_stride": (ctypes.c_int64 * 2)(-16, 16)}, _ext.H3A_EINVAL, "non-negative strides"),
     ],
@@ -449,6 +451,8 @@ def _proj_args(n_sections=3, **overrides):
         ({"sin": (1 << 21) + 8}, _ext.H3A_EINVAL, "16-byte aligned"),
         ({"seqlen": 0}, _ext.H3A_EINVAL, "seqlen"),
         ({"seqlen": 1 << 23}, _ext.H3A_EUNSUPPORTED, "less than 2^32 bytes"),  # 8M rows x 512 bytes
+        ({"table_stride": 1 << 62}, _ext.H3A_EUNSUPPORTED, "less than 2^32 bytes"),  # no 64-bit overflow
+        ({"x_stride": 1 << 61}, _ext.H3A_EUNSUPPORTED, "x_stride too large"),
         ({"m": -1}, _ext.H3A_EINVAL, "extents"),
     ],
 )
@@ -470,6 +474,8 @@ def test_proj_gemm_section_validation(lib):
         ("bias", (1 << 23) + 4, "bias must be 8-byte aligned"),
         ("norm_weight", None, "norm_weight"),
         ("y_stride", 1 << 25, "y_stride too large"),  # 127 rows of 64 MiB pass 2^32 bytes
+        ("y_stride", 1 << 61, "y_stride too large"),  # would overflow a 64-bit product
+        ("weight_stride", 1 << 61, "weight_stride too large"),
     ]:
         a = _proj_args()
         setattr(a.sections[0], field, value)
