@@ -424,10 +424,12 @@ int h3a_pack_qkv(const h3a_pack_qkv_args* a, void* stream) {
     if (!a->q || !a->k || !a->v || !a->out) return fail(H3A_EINVAL, "h3a_pack_qkv: NULL tensor pointer");
     const int64_t* st[3] = {a->q_stride, a->k_stride, a->v_stride};
     const void* src[3] = {a->q, a->k, a->v};
+    if ((__int128)a->rows * a->heads >= ((int64_t)1 << 31) || a->head_dim >= ((int64_t)1 << 30) / es)
+        return fail(H3A_EUNSUPPORTED,
+                    "h3a_pack_qkv: rows=%lld heads=%lld head_dim=%lld: (row, head) units and their bytes must stay "
+                    "under 2^31 and 2^30",
+                    (long long)a->rows, (long long)a->heads, (long long)a->head_dim);
     const int64_t row_bytes = a->head_dim * es;
-    if (a->rows * a->heads >= ((int64_t)1 << 31) || row_bytes >= ((int64_t)1 << 30))
-        return fail(H3A_EUNSUPPORTED, "h3a_pack_qkv: %lld (row, head) units of %lld bytes (limits 2^31, 2^30)",
-                    (long long)(a->rows * a->heads), (long long)row_bytes);
     h3a::PackQkvParams p{};
     bool vec = row_bytes % 16 == 0 && row_bytes <= 4096 && aligned16(a->out);
     for (int i = 0; i < 3; ++i) {
@@ -519,7 +521,7 @@ int h3a_qknorm_rope_pack(const h3a_qknorm_rope_pack_args* a, void* stream) {
         for (int d = 0; d < 2; ++d)
             if (st[i][d] < 0 || st[i][d] % 8 != 0)
                 return fail(H3A_EINVAL, "h3a_qknorm_rope_pack: strides must be non-negative multiples of 8 elements");
-    if (a->rows * 2 * a->heads >= ((int64_t)1 << 31))
+    if ((__int128)a->rows * 2 * a->heads >= ((int64_t)1 << 31))
         return fail(H3A_EUNSUPPORTED, "h3a_qknorm_rope_pack: %lld rows (limit 2^31 / (2 * heads))", (long long)a->rows);
     const int64_t hl = a->heads / a->world;
     const int64_t slot = 3 * D;         // one head's q|k|v in the packed buffer
@@ -643,7 +645,8 @@ int h3a_attn_merge(const h3a_attn_merge_args* a, void* stream) {
     if ((!pf && a->part_dtype != H3A_DTYPE_BF16) || (!of && a->out_dtype != H3A_DTYPE_BF16))
         return fail(H3A_EINVAL, "%s: part and out dtypes must be bf16 or fp32", fn);
     if (a->batch == 0 || a->seqlen == 0) return H3A_OK;
-    if (a->batch * a->seqlen * a->heads >= ((int64_t)1 << 40)) return fail(H3A_EUNSUPPORTED, "%s: too many rows", fn);
+    if ((__int128)a->batch * a->seqlen * a->heads >= ((int64_t)1 << 40))
+        return fail(H3A_EUNSUPPORTED, "%s: too many rows", fn);
     if (!a->o) return fail(H3A_EINVAL, "%s: NULL output", fn);
     const int64_t psz = pf ? 4 : 2, osz = of ? 4 : 2;
     h3a::AttnMergeParams p{};

@@ -191,6 +191,8 @@ def _pack_args(**overrides):
         ({"head_dim": 0}, _ext.H3A_EINVAL, "extents"),
         ({"v": None}, _ext.H3A_EINVAL, "NULL"),
         ({"rows": 1 << 28}, _ext.H3A_EUNSUPPORTED, "2^31"),
+        ({"rows": 1 << 40, "heads": 1 << 40, "world": 1}, _ext.H3A_EUNSUPPORTED, "2^31"),  # no 64-bit wrap
+        ({"head_dim": 1 << 62}, _ext.H3A_EUNSUPPORTED, "2^30"),
     ],
 )
 @host_only
@@ -384,6 +386,7 @@ def _attn_merge_args(**overrides):
         ({"part_dtype": _ext.H3A_DTYPE_I32}, _ext.H3A_EINVAL, "bf16 or fp32"),
         ({"o": None}, _ext.H3A_EINVAL, "NULL output"),
         ({"o": (1 << 24) + 8}, _ext.H3A_EINVAL, "aligned"),
+        ({"batch": 1 << 30, "seqlen": 1 << 30, "heads": 1 << 30}, _ext.H3A_EUNSUPPORTED, "too many rows"),
     ],
 )
 @host_only
