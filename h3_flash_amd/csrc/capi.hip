@@ -393,10 +393,10 @@ int h3a_qknorm_rope(const h3a_qknorm_rope_args* a, void* stream) {
     p.cos = a->cos; p.sin = a->sin; p.table_stride = a->table_stride;
     p.seqlen = (int32_t)a->seqlen; p.heads = (int32_t)a->heads; p.n_tensors = n;
     p.head_dim = (int32_t)D; p.rotary_dim = (int32_t)R; p.w_f32 = a->w_dtype == H3A_DTYPE_F32;
+    if ((__int128)a->batch * a->seqlen * n * a->heads >= ((int64_t)1 << 31) || a->batch > 65535)
+        return fail(H3A_EUNSUPPORTED, "h3a_qknorm_rope: batch %lld x seqlen %lld x %d x heads %lld rows (limits 2^31, batch 65535)",
+                    (long long)a->batch, (long long)a->seqlen, n, (long long)a->heads);
     p.rows = a->batch * a->seqlen * n * a->heads;
-    if (p.rows >= ((int64_t)1 << 31) || a->batch > 65535)
-        return fail(H3A_EUNSUPPORTED, "h3a_qknorm_rope: %lld rows, batch %lld (limits 2^31, 65535)", (long long)p.rows,
-                    (long long)a->batch);
     p.div_heads = h3a::make_fast_div((uint32_t)a->heads);
     p.div_tensors = h3a::make_fast_div((uint32_t)n);
     p.div_seqlen = h3a::make_fast_div((uint32_t)a->seqlen);

@@ -158,6 +158,7 @@ def _rope_args(**overrides):
         ({"table_stride": 64}, _ext.H3A_EINVAL, "table_stride"),
         ({"sin": (1 << 21) + 2}, _ext.H3A_EINVAL, "cos/sin must be 4-byte aligned"),
         ({"abi_version": 0}, _ext.H3A_EINVAL, "abi_version"),
+        ({"seqlen": 1 << 40, "heads": 1 << 40}, _ext.H3A_EUNSUPPORTED, "limits 2^31"),  # no 64-bit wrap
     ],
 )
 @host_only
