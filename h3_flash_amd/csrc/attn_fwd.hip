@@ -625,8 +625,13 @@ __device__ __forceinline__ void attn_tile(Params& p, int tile, int chunk, int ch
 #pragma unroll
         for (int t = 0; t < 4; ++t) kf[t] = kread(2, t);
     }
-    auto step = [&](auto u, int jj) __attribute__((always_inline)) {
+    // kTail: the last two steps of the launch (U = 2, 3 of its last group).
+    // Their QK^T tiles (nsteps, nsteps + 1) and DMA tiles lie past the end,
+    // so they run PV alone, with the softmax of tile nsteps - 1 in step 2.
+    auto step = [&](auto u, int jj, auto tail_c) __attribute__((always_inline)) {
         constexpr int U = decltype(u)::value;
+        constexpr bool kTail = decltype(tail_c)::value;
+        static_assert(!kTail || U >= 2, "only the last two steps of a group skip QK^T");
         // A group of four iterations starts at tile jj: rebase the K / V
         // windows there. Its iterations load K up to tile jj+8 and V up to
         // jj+6, inside the window's kWindowRows.
@@ -648,20 +653,34 @@ __device__ __forceinline__ void attn_tile(Params& p, int tile, int chunk, int ch
             if (k == 16) dma_v1(jv + 3, (U + 3) & 3, 0);
             if (k == 24) dma_v1(jv + 3, (U + 3) & 3, 1);
         };
-        if constexpr (U & 1)
+        if constexpr (kTail) {
+            constexpr std::integral_constant<int, U == 2 ? 1 : 0> sm{};
+            if constexpr (U & 1)
+                iterate(std::false_type{}, sm, std::true_type{}, 0, U, jj + 1, sa, sb, pfb, pfa, -1, no_hook);
+            else
+                iterate(std::false_type{}, sm, std::true_type{}, 0, U, jj + 1, sb, sa, pfa, pfb, -1, no_hook);
+        } else if constexpr (U & 1) {
             iterate(std::true_type{}, kSoftmax, std::true_type{}, (U + 2) & 3, U, jj + 1, sa, sb, pfb, pfa,
                     (U + 3) & 3, hook);
-        else
+        } else {
             iterate(std::true_type{}, kSoftmax, std::true_type{}, (U + 2) & 3, U, jj + 1, sb, sa, pfa, pfb,
                     (U + 3) & 3, hook);
+        }
         wait_vmcnt<2 * kDmaPerTile>();
         barrier();
     };
-    for (int j = 0; j < nsteps; j += 4) {
-        step(std::integral_constant<int, 0>{}, j);
-        step(std::integral_constant<int, 1>{}, j + 1);
-        step(std::integral_constant<int, 2>{}, j + 2);
-        step(std::integral_constant<int, 3>{}, j + 3);
+    int j = 0;
+    for (; j < nsteps - 4; j += 4) {
+        step(std::integral_constant<int, 0>{}, j, std::false_type{});
+        step(std::integral_constant<int, 1>{}, j + 1, std::false_type{});
+        step(std::integral_constant<int, 2>{}, j + 2, std::false_type{});
+        step(std::integral_constant<int, 3>{}, j + 3, std::false_type{});
+    }
+    if (nsteps > 0) {
+        step(std::integral_constant<int, 0>{}, j, std::false_type{});
+        step(std::integral_constant<int, 1>{}, j + 1, std::false_type{});
+        step(std::integral_constant<int, 2>{}, j + 2, std::true_type{});
+        step(std::integral_constant<int, 3>{}, j + 3, std::true_type{});
     }
     wait_vmcnt<0>();  // no LDS DMA may still land after the workgroup ends
 
