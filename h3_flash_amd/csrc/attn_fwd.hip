@@ -71,6 +71,7 @@ constexpr float kRecomputeLimit = 0x1p64f;
 // 32-bit buffer offsets only ever cover one window of the view, however long
 // the view is.
 constexpr int kWindowRows = kBN * 9;
+constexpr int kPersistMaxQTiles = 8;  // longest segment of a persistent launch: 2,048 rows
 constexpr int kQueuePieces = 4;                  // key-range pieces per tile of a dynamic tail
 // Fewest key tiles in such a piece: each piece pays a pipeline fill and
 // drain and a partial result, which short pieces do not recover (8 x 8,192-row
@@ -155,9 +156,19 @@ __device__ __forceinline__ char* attn_lds() {
     return smem;
 }
 
-template <bool kWide, bool kVT, typename Params>
-__device__ __forceinline__ void attn_tile(Params& p, int tile, int chunk, int chunks, int slot,
-                                          bool graded = false) {
+// kPersist (packed launches without a work list, neither wide nor d-major
+// V): qcarry holds Q across calls; `prefetched` says that the previous call
+// already issued this tile's Q loads and its first K / V DMA, and next_tile
+// (-1: none) is the tile whose first loads this call issues in its last two
+// iterations. cu_cur and cu_next hold cu_q[s], cu_q[s + 1], cu_k[s],
+// cu_k[s + 1] of this tile's and the next tile's segment, loaded by the
+// caller one tile ahead. Returns whether it issued the next tile's loads.
+template <bool kWide, bool kVT, bool kPersist = false, typename Params>
+__device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int chunks, int slot,
+                                          bool graded = false, bf16x8* qcarry = nullptr, bool prefetched = false,
+                                          int next_tile = -1, const int* cu_cur = nullptr,
+                                          const int* cu_next = nullptr) {
+    static_assert(!kPersist || (!kWide && !kVT), "persistent launches use the narrow token-major form");
     char* const smem = attn_lds();
     // V stages 0..3 first, then K stages 0..3: with a per-lane base in a VGPR
     // every fragment read offset then fits the 16-bit ds_read immediate.
@@ -188,14 +199,26 @@ __device__ __forceinline__ void attn_tile(Params& p, int tile, int chunk, int ch
         // Segment bounds are clamped to the packed rows, so no cu_seqlens
         // content can move an access outside the tensors.
         b = 0;
-        q0 = min(max(p.cu_q[grp], 0), p.seqlen_q);
-        sq = min(max(p.cu_q[grp + 1], q0), p.seqlen_q) - q0;
-        k0 = min(max(p.cu_k[grp], 0), p.seqlen_k);
-        sk = min(max(p.cu_k[grp + 1], k0), p.seqlen_k) - k0;
+        int cq0, cq1, ck0, ck1;
+        if constexpr (kPersist) {
+            cq0 = __builtin_amdgcn_readfirstlane(cu_cur[0]);
+            cq1 = __builtin_amdgcn_readfirstlane(cu_cur[1]);
+            ck0 = __builtin_amdgcn_readfirstlane(cu_cur[2]);
+            ck1 = __builtin_amdgcn_readfirstlane(cu_cur[3]);
+        } else {
+            cq0 = p.cu_q[grp];
+            cq1 = p.cu_q[grp + 1];
+            ck0 = p.cu_k[grp];
+            ck1 = p.cu_k[grp + 1];
+        }
+        q0 = min(max(cq0, 0), p.seqlen_q);
+        sq = min(max(cq1, q0), p.seqlen_q) - q0;
+        k0 = min(max(ck0, 0), p.seqlen_k);
+        sk = min(max(ck1, k0), p.seqlen_k) - k0;
         if (kVT) vpad = vt_segment_start(k0, grp) - k0;
     }
     const int m0 = qt * kBM;
-    if (m0 >= sq) return;  // whole workgroup: tile beyond this segment
+    if (m0 >= sq) return false;  // whole workgroup: tile beyond this segment
     if (chunk >= 0) {
         // Piece c of n covers key tiles [c*nkt/n, (c+1)*nkt/n). Graded
         // pieces (a queue's 4-way split of long key ranges) cover 3/8, 3/8,
@@ -256,15 +279,27 @@ __device__ __forceinline__ void attn_tile(Params& p, int tile, int chunk, int ch
     // Q fragment: lane holds query row (m0 + 32*wave + l32), head dims
     // 16*ks + 8*hi .. +8 for ks = 0..7 (B operand of S^T = K Q^T).
     const int mq = m0 + wave * 32 + l32;
-    bf16x8 qf[8];
+    bf16x8 qf_own[8];
+    bf16x8(&qf)[8] = *(kPersist ? (bf16x8(*)[8])qcarry : &qf_own);
+    const bool issue = !kPersist || !prefetched;  // false: the previous tile issued Q and the first K / V
+    if (kPersist && issue) {
+        // Q is carried across the loop of a persistent launch, where the
+        // compiler may copy its registers: compiler-tracked loads, which it
+        // waits for before any copy or use.
+        const __amdgpu_buffer_rsrc_t rqb = make_rsrc(qb, span_bytes(sq, p.q_rs));
 #pragma unroll
-    for (int ks = 0; ks < 8; ++ks) {
-        i32x4 raw;
-        asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen"
-                     : "=v"(raw)
-                     : "v"((uint32_t)((mq - q_first) * p.q_rs + ks * 32 + hi * 16)), "s"(rq)
-                     : "memory");
-        qf[ks] = __builtin_bit_cast(bf16x8, raw);
+        for (int ks = 0; ks < 8; ++ks)
+            qf[ks] = __builtin_bit_cast(bf16x8, buf_load16(rqb, (uint32_t)(mq * p.q_rs + ks * 32 + hi * 16)));
+    } else if (issue) {
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) {
+            i32x4 raw;
+            asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen"
+                         : "=v"(raw)
+                         : "v"((uint32_t)((mq - q_first) * p.q_rs + ks * 32 + hi * 16)), "s"(rq)
+                         : "memory");
+            qf[ks] = __builtin_bit_cast(bf16x8, raw);
+        }
     }
 
     // DMA map: wave w fills rows 8w .. 8w+7 of a tile with two 4-row loads;
@@ -599,13 +634,18 @@ __device__ __forceinline__ void attn_tile(Params& p, int tile, int chunk, int ch
     constexpr std::integral_constant<int, 2> kFirstSoftmax{};
     const int nsteps = (ntiles + 3) & ~3;
     if (ntiles > 0) {
-        dma_k(0, 0);
-        dma_k(1, 1);
-        dma_v(0, 0);
-        dma_k(2, 2);
-        dma_v(1, 1);
-        dma_k(3, 3);
-        dma_v(2, 2);
+        if (issue) {
+            dma_k(0, 0);
+            dma_k(1, 1);
+            dma_v(0, 0);
+            dma_k(2, 2);
+            dma_v(1, 1);
+            dma_k(3, 3);
+            dma_v(2, 2);
+        }
+        // Prefetched by the previous tile, in this order, before that
+        // tile's O stores: the stores are younger, so each wait below only
+        // gets stronger.
         wait_vmcnt<6 * kDmaPerTile>();  // Q and K_0 have landed
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) asm volatile("" : "+v"(qf[ks]));  // no Q use before the wait
@@ -625,6 +665,53 @@ __device__ __forceinline__ void attn_tile(Params& p, int tile, int chunk, int ch
 #pragma unroll
         for (int t = 0; t < 4; ++t) kf[t] = kread(2, t);
     }
+    // Persistent launches: the first PV-only iteration issues the next
+    // tile's Q loads (Q's registers are dead after the last QK^T) and its
+    // K_0..K_3 and V_0, V_1 DMA (the K stages and V stages 0, 1 are no longer
+    // read), in the order of the prologue above; the second issues V_2 into
+    // stage 2, which the first one's PV read. The vmcnt(0) first lets the
+    // past-end DMA of this tile land before the same rows are written again.
+    // The Q loads are compiler builtins, so the compiler waits for them
+    // before any use or copy of their registers.
+    bool pref = false;
+    i32x4 nrv{};
+    auto prefetch = [&]() __attribute__((always_inline)) {
+        if constexpr (kPersist) {
+            if (next_tile < 0) return;
+            const int nqt = next_tile % p.n_qtiles;
+            const int nh = (next_tile / p.n_qtiles) % p.heads;
+            const int nq0 = min(max(__builtin_amdgcn_readfirstlane(cu_next[0]), 0), p.seqlen_q);
+            const int nsq = min(max(__builtin_amdgcn_readfirstlane(cu_next[1]), nq0), p.seqlen_q) - nq0;
+            const int nk0 = min(max(__builtin_amdgcn_readfirstlane(cu_next[2]), 0), p.seqlen_k);
+            const int nsk = min(max(__builtin_amdgcn_readfirstlane(cu_next[3]), nk0), p.seqlen_k) - nk0;
+            const int nm0 = nqt * kBM;
+            if (nm0 >= nsq || nsk <= 0) return;  // the next call issues nothing either
+            wait_vmcnt<0>();
+            const char* nqb = (const char*)p.q + 2 * (nh * p.q_sh) + (int64_t)nq0 * p.q_rs;
+            const char* nkb = (const char*)p.k + 2 * (nh * p.k_sh) + (int64_t)nk0 * p.k_rs;
+            const char* nvb = (const char*)p.v + 2 * (nh * p.v_sh) + (int64_t)nk0 * p.v_rs;
+            const __amdgpu_buffer_rsrc_t nrq = make_rsrc(nqb, span_bytes(nsq, p.q_rs));
+            const i32x4 nrk = make_rsrc_words(nkb, span_bytes(nsk, p.k_rs));
+            nrv = make_rsrc_words(nvb, span_bytes(nsk, p.v_rs));
+            const int nmq = nm0 + wave * 32 + l32;
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks)
+                qf[ks] = __builtin_bit_cast(bf16x8, buf_load16(nrq, (uint32_t)(nmq * p.q_rs + ks * 32 + hi * 16)));
+#pragma unroll
+            for (int i = 0; i < kDmaPerTile; ++i) dma1(nrk, p.k_rs, dk, kst + 0 * kTile, 0, i);
+#pragma unroll
+            for (int i = 0; i < kDmaPerTile; ++i) dma1(nrk, p.k_rs, dk, kst + 1 * kTile, 1, i);
+#pragma unroll
+            for (int i = 0; i < kDmaPerTile; ++i) dma1(nrv, p.v_rs, dv, vst + 0 * kTile, 0, i);
+#pragma unroll
+            for (int i = 0; i < kDmaPerTile; ++i) dma1(nrk, p.k_rs, dk, kst + 2 * kTile, 2, i);
+#pragma unroll
+            for (int i = 0; i < kDmaPerTile; ++i) dma1(nrv, p.v_rs, dv, vst + 1 * kTile, 1, i);
+#pragma unroll
+            for (int i = 0; i < kDmaPerTile; ++i) dma1(nrk, p.k_rs, dk, kst + 3 * kTile, 3, i);
+            pref = true;
+        }
+    };
     // kTail: the last two steps of the launch (U = 2, 3 of its last group).
     // Their QK^T tiles (nsteps, nsteps + 1) and DMA tiles lie past the end,
     // so they run PV alone, with the softmax of tile nsteps - 1 in step 2.
@@ -655,6 +742,13 @@ __device__ __forceinline__ void attn_tile(Params& p, int tile, int chunk, int ch
         };
         if constexpr (kTail) {
             constexpr std::integral_constant<int, U == 2 ? 1 : 0> sm{};
+            if constexpr (kPersist && U == 2) prefetch();
+            if constexpr (kPersist && U == 3) {
+                if (pref) {
+#pragma unroll
+                    for (int i = 0; i < kDmaPerTile; ++i) dma1(nrv, p.v_rs, dv, vst + 2 * kTile, 2, i);
+                }
+            }
             if constexpr (U & 1)
                 iterate(std::false_type{}, sm, std::true_type{}, 0, U, jj + 1, sa, sb, pfb, pfa, -1, no_hook);
             else
@@ -666,7 +760,9 @@ __device__ __forceinline__ void attn_tile(Params& p, int tile, int chunk, int ch
             iterate(std::true_type{}, kSoftmax, std::true_type{}, (U + 2) & 3, U, jj + 1, sb, sa, pfa, pfb,
                     (U + 3) & 3, hook);
         }
-        wait_vmcnt<2 * kDmaPerTile>();
+        // The tail steps issue none of this tile's loads (and a persistent
+        // launch's prefetch must stay in flight).
+        if constexpr (!(kPersist && kTail)) wait_vmcnt<2 * kDmaPerTile>();
         barrier();
     };
     int j = 0;
@@ -682,7 +778,7 @@ __device__ __forceinline__ void attn_tile(Params& p, int tile, int chunk, int ch
         step(std::integral_constant<int, 2>{}, j + 2, std::true_type{});
         step(std::integral_constant<int, 3>{}, j + 3, std::true_type{});
     }
-    wait_vmcnt<0>();  // no LDS DMA may still land after the workgroup ends
+    if (!pref) wait_vmcnt<0>();  // no LDS DMA may still land after the workgroup ends (a prefetch lands for the next tile)
 
     // Epilogue: combine the two halves' partial sums, normalise, store.
     {
@@ -704,7 +800,7 @@ __device__ __forceinline__ void attn_tile(Params& p, int tile, int chunk, int ch
                                           oacc[db][i * 4 + 2] * inv, oacc[db][i * 4 + 3] * inv};
             }
         if (hi == 0) p.ws_lse[(int64_t)slot * kBM + row] = lse;
-        return;
+        return false;
     }
     if (mq < sq) {
         char* ob = (char*)p.o + 2 * (b * p.o_sb + h * p.o_sh) + (int64_t)(q0 + mq) * p.o_rs;
@@ -720,6 +816,7 @@ __device__ __forceinline__ void attn_tile(Params& p, int tile, int chunk, int ch
             }
         if (p.lse != nullptr && hi == 0) p.lse[b * p.lse_sb + h * p.lse_sh + q0 + mq] = lse;
     }
+    return pref;
 }
 
 // The dynamic tail: the last round's tiles are cut into key-range pieces
@@ -847,6 +944,63 @@ __device__ __forceinline__ int block_scan(int v, int* buf, int* total) {
     *total = buf[255];
     __syncthreads();
     return incl - v;
+}
+
+// Packed launches of short segments without a work list: one workgroup per CU
+// runs tile after tile, and each tile issues the next one's Q loads and first
+// K / V DMA during its own last two iterations, so the next tile starts with
+// them in flight or landed instead of paying their latency (5-7 us against
+// 1.5 us per key tile). Tiles [0, grid) start one per workgroup; every later
+// one is claimed from the counter at p.persist_queue (tile grid + claim),
+// two tiles ahead of its run, so the claim's latency passes during a tile and
+// workgroups that drew short tiles take more of them.
+__global__ __launch_bounds__(kThreads, 2) void attn_fwd_persist_kernel(AttnParams p) {
+    __shared__ int claim;
+    const int total = p.n_qtiles * p.heads * p.n_groups;
+    const int grid = (int)gridDim.x;
+    // Segment bounds of tile t, loaded one tile ahead: they have landed when
+    // the tile starts, and the next tile's by the time its loads are issued.
+    // Read through the constant address space (nothing writes them during
+    // the launch): scalar loads, which vector-memory waits do not count.
+    using ConstInt = const __attribute__((address_space(4))) int;
+    ConstInt* const cq = (ConstInt*)(uintptr_t)p.cu_q;
+    ConstInt* const ck = (ConstInt*)(uintptr_t)p.cu_k;
+    auto bounds = [&](int t, int* c) {
+        const int s = t / p.n_qtiles / p.heads;
+        c[0] = cq[s];
+        c[1] = cq[s + 1];
+        c[2] = ck[s];
+        c[3] = ck[s + 1];
+    };
+    // Every wave reads the claim before thread 0 writes the next one.
+    auto broadcast = [&](int c) {
+        if (threadIdx.x == 0) claim = c;
+        __syncthreads();
+        const int v = __builtin_amdgcn_readfirstlane(claim);
+        __syncthreads();
+        return grid + v < total ? grid + v : -1;
+    };
+    int t = blockIdx.x;  // grid <= total
+    int nt = broadcast(threadIdx.x == 0 ? atomicAdd(p.persist_queue, 1) : 0);
+    bf16x8 qf[8];
+    int cur[4], nxt[4];
+    bool pre = false;
+    bounds(t, cur);
+    for (;;) {
+        bounds(nt >= 0 ? nt : t, nxt);
+        int c_after = 0;
+        if (nt >= 0 && threadIdx.x == 0) c_after = atomicAdd(p.persist_queue, 1);
+        // The arguments through an opaque address, as in the tail loop above.
+        int zero;
+        asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
+        KernArgs* pk = (KernArgs*)((const __attribute__((address_space(4))) char*)&p + zero);
+        pre = attn_tile<false, false, true>(*pk, t, -1, 1, -1, false, qf, pre, nt, cur, nxt);
+        if (nt < 0) break;
+        t = nt;
+        nt = broadcast(c_after);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cur[i] = nxt[i];
+    }
 }
 
 __global__ __launch_bounds__(256) void attn_varlen_plan_kernel(AttnParams p) {
@@ -1103,6 +1257,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
 }  // namespace
 
 int attn_fwd_block_m() { return kBM; }
+int attn_fwd_persist_max_rows() { return kPersistMaxQTiles * kBM; }
 int attn_fwd_tail_pieces() { return kQueuePieces; }
 int64_t attn_fwd_piece_bytes() { return (int64_t)kBM * (kD + 1) * (int64_t)sizeof(float); }
 int attn_fwd_block_n() { return kBN; }
@@ -1200,7 +1355,17 @@ hipError_t launch_attn_fwd(const AttnParams& p, hipStream_t stream) {
         const dim3 tgrid((unsigned)vt_tiles, (unsigned)p.heads, (unsigned)(p.cu_k != nullptr ? 1 : p.n_groups));
         hipLaunchKernelGGL(attn_vt_kernel, tgrid, dim3(256), 0, stream, p);
     }
-    const dim3 grid((unsigned)blocks), block(kThreads);
+    const dim3 block(kThreads);
+    // Persistent only for short segments (at most kPersistMaxQTiles query
+    // tiles each), where a tile's fixed cost is a large share of it.
+    if (p.cu_q != nullptr && p.vplan == nullptr && !p.wide && p.vt == nullptr && p.split_n == 0 &&
+        p.queue == nullptr && p.persist_queue != nullptr && p.persist_blocks > 0 && p.n_qtiles <= kPersistMaxQTiles) {
+        const int64_t n = blocks < p.persist_blocks ? blocks : p.persist_blocks;
+        hipLaunchKernelGGL(attn_queue_reset, dim3(1), dim3(64), 0, stream, p.persist_queue);
+        hipLaunchKernelGGL(attn_fwd_persist_kernel, dim3((unsigned)n), block, 0, stream, p);
+        return hipGetLastError();
+    }
+    const dim3 grid((unsigned)blocks);
     if (p.wide && p.vt != nullptr)
         hipLaunchKernelGGL((attn_fwd_kernel<true, true>), grid, block, 0, stream, p);
     else if (p.wide)

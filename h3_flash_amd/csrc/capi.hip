@@ -164,11 +164,12 @@ struct AttnWorkspace {
     int64_t plan_offset;
     int32_t ub_tiles, cus;
     int64_t total;
+    bool persist;  // short packed segments: a tile counter at offset 0
 };
 
 AttnWorkspace attn_workspace(const h3a_attn_args* a, const h3a::AttnParams& p, bool allow_vt,
                              int64_t max_workspace = INT64_MAX) {
-    AttnWorkspace w{attn_plan(a, p, max_workspace), 0, 0, 0, 0, 0, 0};
+    AttnWorkspace w{attn_plan(a, p, max_workspace), 0, 0, 0, 0, 0, 0, false};
     w.total = w.plan.workspace_bytes;
     const int bn = h3a::attn_fwd_block_n();
     if (a->cu_seqlens_q != nullptr) {
@@ -178,7 +179,16 @@ AttnWorkspace attn_workspace(const h3a_attn_args* a, const h3a::AttnParams& p, b
         // Only for segments long enough that a balanced last round pays for
         // the planning launch (max_seqlen_q bounds them).
         const int cus = device_cus();
-        if (!allow_vt || cus <= 0 || a->max_seqlen_q < kPlanMinSegment) return w;
+        if (!allow_vt || cus <= 0) return w;
+        if (a->max_seqlen_q < kPlanMinSegment) {
+            // Short segments: the persistent launch's tile counter.
+            if (a->max_seqlen_q <= h3a::attn_fwd_persist_max_rows() && w.total + 256 <= max_workspace) {
+                w.persist = true;
+                w.cus = cus;
+                w.total += 256;
+            }
+            return w;
+        }
         const int64_t nseg = a->num_segments, bm = h3a::attn_fwd_block_m();
         const int64_t grid = (int64_t)p.n_qtiles * p.heads * p.n_groups;
         int64_t ub = a->heads * ((a->seqlen_q + bm - 1) / bm + nseg);
@@ -187,7 +197,7 @@ AttnWorkspace attn_workspace(const h3a_attn_args* a, const h3a::AttnParams& p, b
         const int64_t words = h3a::kPlanWords + ub + 2 * pieces + 2 * cus + 4 * nseg;
         w.plan_offset = pieces * h3a::attn_fwd_piece_bytes();
         w.total = w.plan_offset + (4 * words + 255) / 256 * 256;
-        if (w.total > max_workspace) return AttnWorkspace{w.plan, 0, 0, 0, 0, 0, 0};
+        if (w.total > max_workspace) return AttnWorkspace{w.plan, 0, 0, 0, 0, 0, 0, false};
         w.ub_tiles = (int32_t)ub;
         w.cus = cus;
         const int64_t vt_rs = ((a->seqlen_k + bn - 1) / bn * bn + bn * nseg) * 2;
@@ -287,6 +297,10 @@ int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
     const AttnWorkspace w = attn_workspace(a, p, true);
     if (w.total > 0 && a->workspace != nullptr && a->workspace_bytes >= w.total && ((uintptr_t)a->workspace & 255u) == 0) {
         if (w.plan.split_n != 0) apply_plan(p, w.plan, a->workspace);
+        if (w.persist) {
+            p.persist_queue = (int*)a->workspace;
+            p.persist_blocks = w.cus;
+        }
         if (w.ub_tiles > 0) {
             const int64_t pieces = (int64_t)h3a::attn_fwd_tail_pieces() * w.cus;
             p.ws_o = (float*)a->workspace;

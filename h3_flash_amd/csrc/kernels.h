@@ -70,6 +70,12 @@ struct AttnParams {
     int32_t* vscratch;       // 4 * num_segments words of the planning kernel
     int32_t ub_tiles;
     int32_t plan_cus;
+    // Packed launches of short segments without a work list (persist_queue
+    // != NULL): at most persist_blocks persistent workgroups claim tiles from
+    // the counter *persist_queue, which the launch zeroes. NULL: one
+    // workgroup per tile.
+    int* persist_queue;
+    int32_t persist_blocks;
 };
 
 // Words of the planned-varlen header (vplan).
@@ -92,6 +98,8 @@ constexpr int64_t kStaticScratchBytes = H3A_NOALLOC_SCRATCH_BYTES;
 hipError_t attn_static_scratch(void** ptr);
 
 int attn_fwd_block_m();
+// Longest segment (max_seqlen_q) of a persistent packed launch.
+int attn_fwd_persist_max_rows();
 // Most key-range pieces per tile of a tail, and the workspace bytes of one
 // piece's fp32 partial O and LSE.
 int attn_fwd_tail_pieces();

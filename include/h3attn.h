@@ -109,7 +109,12 @@ extern "C" {
  *     longest segments first; the last round's tiles as key-range pieces
  *     taken from a counter, merged as above), and the d-major V with each
  *     segment padded to 64 keys. Any cu_seqlens contents keep every access
- *     in bounds; offsets that do not ascend give undefined rows.
+ *     in bounds; offsets that do not ascend give undefined rows;
+ *   - packed varlen with max_seqlen_q of at most 2,048: 256 bytes, the tile
+ *     counter of a persistent launch (one workgroup per CU claims tile after
+ *     tile and issues each next tile's first loads during its current one;
+ *     the counter is zeroed by a small kernel first). Results are
+ *     bit-identical to one workgroup per tile.
  * With a NULL or smaller workspace every tile runs whole on V as given. The
  * results differ only by rounding. Calls sharing one workspace must be
  * ordered (same stream).

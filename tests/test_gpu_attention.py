@@ -531,3 +531,37 @@ def test_full_size_properties(name):
     o3, l3 = flash_attn_func(q, k, v)
     assert torch.equal(o3, out) and torch.equal(l3, lse)
     torch.cuda.synchronize()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("seed,n_seg,max_len", [(0, 300, 2048), (1, 700, 512), (2, 40, 300)])
+def test_persistent_short_segments_match_dispatch_order(seed, n_seg, max_len):
+    """Packed short segments (at most 2,048 rows) with a workspace run on
+    persistent workgroups that claim tiles from a counter and prefetch each
+    next tile's Q and first K / V during the current tile's last iterations.
+    Many tiles per workgroup, ragged lengths, empty segments and one-row
+    segments: outputs and LSE match the one-workgroup-per-tile launch
+    (split_tail=False, no workspace) bit for bit, and sampled segments match
+    the oracle."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(0, max_len + 1, (n_seg,), generator=g)
+    lens[0], lens[-1] = max_len, 1
+    lens[n_seg // 2] = 0
+    H = 2
+    cu = torch.zeros(n_seg + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lens, 0)
+    S = int(cu[-1])
+    q, k, v = (_rand((1, S, H, 128), seed * 3 + i).to(DEV) for i in range(3))
+    cu_d = cu.to(DEV)
+    kw = dict(cu_seqlens_q=cu_d, cu_seqlens_k=cu_d, max_seqlen_q=int(lens.max()))
+    o_p, l_p = flash_attn_func(q, k, v, **kw)
+    o_d, l_d = flash_attn_func(q, k, v, split_tail=False, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o_p, o_d)
+    assert torch.equal(l_p, l_d)
+    for s in (0, 1, n_seg // 3, n_seg - 1):
+        a, b = int(cu[s]), int(cu[s + 1])
+        if b == a:
+            continue
+        ref_o, ref_l = sdpa_reference(q[:, a:b].cpu(), k[:, a:b].cpu(), v[:, a:b].cpu())
+        assert_parity(o_p[:, a:b].cpu(), l_p[..., a:b].cpu(), ref_o, ref_l, ("segment", s, b - a))
