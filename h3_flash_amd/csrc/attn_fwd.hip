@@ -71,7 +71,7 @@ constexpr float kRecomputeLimit = 0x1p64f;
 // 32-bit buffer offsets only ever cover one window of the view, however long
 // the view is.
 constexpr int kWindowRows = kBN * 9;
-constexpr int kPersistMaxQTiles = 8;  // longest segment of a persistent launch: 2,048 rows
+constexpr int kPersistMaxQTiles = 16;  // longest segment of a persistent launch: 4,096 rows
 constexpr int kQueuePieces = 4;                  // key-range pieces per tile of a dynamic tail
 // Fewest key tiles in such a piece: each piece pays a pipeline fill and
 // drain and a partial result, which short pieces do not recover (8 x 8,192-row

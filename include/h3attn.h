@@ -110,7 +110,7 @@ extern "C" {
  *     taken from a counter, merged as above), and the d-major V with each
  *     segment padded to 64 keys. Any cu_seqlens contents keep every access
  *     in bounds; offsets that do not ascend give undefined rows;
- *   - packed varlen with max_seqlen_q of at most 2,048: 256 bytes, the tile
+ *   - packed varlen with max_seqlen_q below 4,096: 256 bytes, the tile
  *     counter of a persistent launch (one workgroup per CU claims tile after
  *     tile and issues each next tile's first loads during its current one;
  *     the counter is zeroed by a small kernel first). Results are

@@ -534,9 +534,9 @@ def test_full_size_properties(name):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("seed,n_seg,max_len", [(0, 300, 2048), (1, 700, 512), (2, 40, 300)])
+@pytest.mark.parametrize("seed,n_seg,max_len", [(0, 300, 2048), (1, 700, 512), (2, 40, 300), (3, 90, 4000)])
 def test_persistent_short_segments_match_dispatch_order(seed, n_seg, max_len):
-    """Packed short segments (at most 2,048 rows) with a workspace run on
+    """Packed short segments (fewer than 4,096 rows) with a workspace run on
     persistent workgroups that claim tiles from a counter and prefetch each
     next tile's Q and first K / V during the current tile's last iterations.
     Many tiles per workgroup, ragged lengths, empty segments and one-row
