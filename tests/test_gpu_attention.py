@@ -565,3 +565,40 @@ def test_persistent_short_segments_match_dispatch_order(seed, n_seg, max_len):
             continue
         ref_o, ref_l = sdpa_reference(q[:, a:b].cpu(), k[:, a:b].cpu(), v[:, a:b].cpu())
         assert_parity(o_p[:, a:b].cpu(), l_p[..., a:b].cpu(), ref_o, ref_l, ("segment", s, b - a))
+
+
+@pytest.mark.gpu
+def test_persistent_cross_segments_with_empty_key_ranges():
+    """Packed cross attention on the persistent launch: query and key
+    segments of different lengths, some key ranges empty (those rows give
+    O = 0 and LSE = -inf) and some query ranges empty, many tiles per
+    workgroup. The next-tile prefetch skips tiles without keys. Bit for bit
+    equal to one workgroup per tile, and sampled segments match the oracle."""
+    g = torch.Generator().manual_seed(11)
+    n_seg, H = 400, 2
+    lq = torch.randint(0, 1500, (n_seg,), generator=g)
+    lk = torch.randint(0, 3000, (n_seg,), generator=g)
+    lk[::7] = 0
+    lq[::11] = 0
+    lq[1], lk[1] = 1400, 0
+    cq = torch.zeros(n_seg + 1, dtype=torch.int32)
+    ck = torch.zeros(n_seg + 1, dtype=torch.int32)
+    cq[1:], ck[1:] = torch.cumsum(lq, 0), torch.cumsum(lk, 0)
+    q = _rand((1, int(cq[-1]), H, 128), 21).to(DEV)
+    k = _rand((1, int(ck[-1]), H, 128), 22).to(DEV)
+    v = _rand((1, int(ck[-1]), H, 128), 23).to(DEV)
+    kw = dict(cu_seqlens_q=cq.to(DEV), cu_seqlens_k=ck.to(DEV), max_seqlen_q=int(lq.max()))
+    o_p, l_p = flash_attn_func(q, k, v, **kw)
+    o_d, l_d = flash_attn_func(q, k, v, split_tail=False, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o_p, o_d)
+    assert torch.equal(l_p, l_d)
+    a, b = int(cq[1]), int(cq[2])
+    assert torch.count_nonzero(o_p[:, a:b]).item() == 0
+    assert bool(torch.isneginf(l_p[..., a:b]).all())
+    for s in (0, 2, n_seg // 2, n_seg - 2):
+        qa, qb, ka, kb = int(cq[s]), int(cq[s + 1]), int(ck[s]), int(ck[s + 1])
+        if qb == qa or kb == ka:
+            continue
+        ref_o, ref_l = sdpa_reference(q[:, qa:qb].cpu(), k[:, ka:kb].cpu(), v[:, ka:kb].cpu())
+        assert_parity(o_p[:, qa:qb].cpu(), l_p[..., qa:qb].cpu(), ref_o, ref_l, ("segment", s))
