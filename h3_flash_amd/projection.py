@@ -27,6 +27,7 @@ own norms.
 from __future__ import annotations
 
 import ctypes
+import weakref
 from typing import Any
 
 import torch
@@ -106,25 +107,30 @@ def proj_gemm(
         raise RuntimeError(message)
 
 
-# Tables already checked for the rotate-half form, by identity and version.
-_HALF_CHECKED: dict[tuple, bool] = {}
+# Attribute under which a cos table object remembers its last check: (a weak
+# reference to the sin table it was checked with, both tables' versions, the
+# answer). It lives on the tensor object itself, so a later table that reuses
+# a freed table's memory (the caching allocator hands addresses out again,
+# and a new tensor starts at version 0) never sees an earlier answer.
+_HALF_ATTR = "_h3a_rotate_half"
 
 
 def rotate_half_tables(cos: torch.Tensor, sin: torch.Tensor) -> bool:
     """Whether columns ``c`` and ``c + R/2`` of both tables are equal (one
-    device comparison per table version, then cached)."""
+    device comparison per pair of table objects and versions, then cached on
+    the cos tensor)."""
 
     R = cos.shape[-1]
     if R % 2 or sin.shape != cos.shape:
         return False
-    key = (cos.data_ptr(), cos._version, sin.data_ptr(), sin._version, tuple(cos.shape), cos.device)
-    hit = _HALF_CHECKED.get(key)
-    if hit is None:
-        h = R // 2
-        hit = bool(torch.equal(cos[..., :h], cos[..., h:]) and torch.equal(sin[..., :h], sin[..., h:]))
-        if len(_HALF_CHECKED) > 64:
-            _HALF_CHECKED.clear()
-        _HALF_CHECKED[key] = hit
+    memo = getattr(cos, _HALF_ATTR, None)
+    if memo is not None:
+        sin_ref, cos_ver, sin_ver, hit = memo
+        if sin_ref() is sin and cos_ver == cos._version and sin_ver == sin._version:
+            return hit
+    h = R // 2
+    hit = bool(torch.equal(cos[..., :h], cos[..., h:]) and torch.equal(sin[..., :h], sin[..., h:]))
+    setattr(cos, _HALF_ATTR, (weakref.ref(sin), cos._version, sin._version, hit))
     return hit
 
 
@@ -185,12 +191,14 @@ def qkv_projection(
     cos, sin = rotary_emb
     if cos.dim() != 2 or cos.shape[0] != S or cos.shape[-1] % 32 or cos.shape[-1] > HEAD_DIM or sin.shape != cos.shape:
         return None
+    # Checked on the caller's own table objects (the conversions below may
+    # make fresh temporaries); a dtype or layout change keeps the form.
+    if not rotate_half_tables(cos, sin):
+        return None
     cos = cos.to(device=x.device, dtype=torch.float32)
     sin = sin.to(device=x.device, dtype=torch.float32)
     if not (cos.is_contiguous() and sin.is_contiguous()):
         cos, sin = cos.contiguous(), sin.contiguous()
-    if not rotate_half_tables(cos, sin):
-        return None
     wq_n, wk_n = (t.to(x.device) for t in (wq_n, wk_n))
     out = torch.empty((B, S, 3 * n), dtype=torch.bfloat16, device=x.device)
     y = out.view(B * S, 3 * n)
