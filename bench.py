@@ -32,6 +32,7 @@ sys.path.insert(0, str(ROOT))
 
 METRIC = "attn TFLOP/s + % bf16 MFMA peak, S=49,920 H=5 D=128 non-causal, 1 MI355X"
 PEAK_BF16_TFLOPS = 2516.6  # MI355X dense bf16 MFMA: 256 CU x 4 SIMD x 1024 flop/clk x 2.4 GHz
+PEAK_SCLK_MHZ = 2400.0  # the engine clock the nominal peak is quoted at
 PEAK_HBM_GBS = 8000.0
 PMC_SUMMARY = ROOT / "profiles" / "attn_fwd_c2_pmc.txt"
 
@@ -562,7 +563,7 @@ def main(argv=None) -> int:
 
     import torch
 
-    from h3_flash_amd import flash_attn_func
+    from h3_flash_amd import devclock, flash_attn_func
     from h3_flash_amd.prologue import fused_qk_norm_rope
     from h3_flash_amd.synth import WORKLOADS, make_raw
 
@@ -617,6 +618,9 @@ def main(argv=None) -> int:
     region0 = torch.cuda.Event(enable_timing=True)
     region1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    # Per-CU cycle counters just outside the timed region (one small launch
+    # on each side): the core clock the part held over the timed launches.
+    clock0 = devclock.sample(torch, dev)
     wall0 = time.perf_counter()
     region0.record(stream)
     for a, b in events:
@@ -624,7 +628,10 @@ def main(argv=None) -> int:
         step()
         b.record(stream)
     region1.record(stream)
+    clock1 = devclock.sample(torch, dev)
     torch.cuda.synchronize()
+    clock = devclock.mean_clock(clock0.cpu(), clock1.cpu())
+    sclk = clock.get("sclk_mhz")
     wall = time.perf_counter() - wall0
     region_ms = region0.elapsed_time(region1)
     launch_ms = [a.elapsed_time(b) for a, b in events]
@@ -668,12 +675,20 @@ def main(argv=None) -> int:
             "parallelism": "single GPU (one head shard, no collectives)",
         },
         "pct_of_peak": 100.0 * value / PEAK_BF16_TFLOPS,
+        # mean core clock of the 256 CUs over the timed launches (per-CU
+        # s_memtime against the 100 MHz s_memrealtime), and the fraction of
+        # the MFMA peak at that clock: frac * 2400 / sclk_mhz
+        "sclk_mhz": sclk,
+        "frac_at_sclk": (value / PEAK_BF16_TFLOPS) * PEAK_SCLK_MHZ / sclk if sclk else None,
+        "clock": clock,
         "roofline": {
             "bound": "mfma",
             "achieved": achieved,
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / PEAK_BF16_TFLOPS,
+            "sclk_mhz": sclk,
+            "frac_at_sclk": (achieved / PEAK_BF16_TFLOPS) * PEAK_SCLK_MHZ / sclk if sclk else None,
             "traffic": traffic,
             "traffic_source": traffic_source,
             "kernel": "attn_fwd_kernel",

@@ -21,7 +21,7 @@ LIB_DIR = PACKAGE_DIR / "_lib"
 LIB_PATH = LIB_DIR / "libh3attn.so"
 INCLUDE_DIR = REPO_DIR / "include"
 
-SOURCES = ("capi.hip", "attn_fwd.hip", "qknorm_rope.hip", "relayout.hip", "fusions.hip", "attn_merge.hip", "proj_gemm.hip")
+SOURCES = ("capi.hip", "attn_fwd.hip", "qknorm_rope.hip", "relayout.hip", "fusions.hip", "attn_merge.hip", "proj_gemm.hip", "clock.hip")
 
 HIPCC_FLAGS = (
     "--offload-arch=gfx950",

@@ -239,6 +239,7 @@ class AttnMergeArgs(ctypes.Structure):
 H3A_PROJ_PLAIN = 0
 H3A_PROJ_QKNORM_ROPE = 1
 H3A_PROJ_MAX_SECTIONS = 3
+H3A_CLOCK_RECORDS = 2048  # records of one h3a_clock_sample launch
 
 
 class ProjSection(ctypes.Structure):
@@ -291,6 +292,7 @@ SIGNATURES = {
     "h3a_swiglu": (ctypes.c_int, [ctypes.POINTER(SwigluArgs), ctypes.c_void_p]),
     "h3a_attn_merge": (ctypes.c_int, [ctypes.POINTER(AttnMergeArgs), ctypes.c_void_p]),
     "h3a_proj_gemm": (ctypes.c_int, [ctypes.POINTER(ProjArgs), ctypes.c_void_p]),
+    "h3a_clock_sample": (ctypes.c_int, [ctypes.c_void_p, ctypes.c_void_p]),
     "h3a_last_error": (ctypes.c_char_p, []),
     "h3a_abi_version": (ctypes.c_int, []),
 }

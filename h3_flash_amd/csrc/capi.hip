@@ -288,6 +288,15 @@ const char* h3a_last_error(void) { return g_err; }
 
 int h3a_abi_version(void) { return H3A_ABI_VERSION; }
 
+int h3a_clock_sample(uint64_t* out, void* stream) {
+    g_err[0] = '\0';
+    if (out == nullptr) return fail(H3A_EINVAL, "h3a_clock_sample: out is NULL");
+    if (((uintptr_t)out & 7u) != 0) return fail(H3A_EINVAL, "h3a_clock_sample: out must be 8-byte aligned");
+    const hipError_t e = h3a::launch_clock_sample(out, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_clock_sample: launch failed: %s", hipGetErrorString(e));
+    return H3A_OK;
+}
+
 int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
     g_err[0] = '\0';
     h3a::AttnParams p{};

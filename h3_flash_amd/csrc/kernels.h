@@ -261,4 +261,7 @@ int proj_gemm_tile();
 int proj_gemm_k_multiple();  // k must be a multiple of this
 hipError_t launch_proj_gemm(const ProjGemmParams& p, hipStream_t stream);
 
+// Clock sample (clock.hip): H3A_CLOCK_RECORDS records of 4 uint64 at out.
+hipError_t launch_clock_sample(uint64_t* out, hipStream_t stream);
+
 }  // namespace h3a

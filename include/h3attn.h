@@ -497,6 +497,28 @@ typedef struct h3a_proj_args {
 
 H3A_API int h3a_proj_gemm(const h3a_proj_args *args, void *stream);
 
+/*
+ * Device clock sample. A measurement aid with no counterpart in the reference
+ * (its benchmark, benchmarks/benchmark_dense_fa4.py:84-136, reports wall time
+ * only); for benchmarks that quote a fraction of the nominal MFMA peak, which
+ * depends on the core clock the part holds under load.
+ *
+ * Launches H3A_CLOCK_RECORDS one-wave workgroups on `stream`, enough for
+ * every CU to run several. Workgroup i writes four values to
+ * out[4*i .. 4*i+3] (a device array of 4 * H3A_CLOCK_RECORDS uint64):
+ *   the XCD it ran on (HW_REG_XCC_ID), its hardware wave id (HW_REG_HW_ID:
+ *   bits 8-15 name the CU within the XCD), the CU's shader clock counter
+ *   (s_memtime, core clock cycles) and the chip's constant 100 MHz realtime
+ *   counter (s_memrealtime).
+ * The cycle counters of different CUs are not aligned with each other, and
+ * a CU's counter advances only while the CU is clocked. Two samples on one
+ * stream around a stretch of work that keeps every CU busy give each CU's
+ * mean core clock over it, from the records of the same (XCD, CU) in both:
+ * 100 MHz * d(memtime) / d(realtime).
+ */
+#define H3A_CLOCK_RECORDS 2048
+H3A_API int h3a_clock_sample(uint64_t *out, void *stream);
+
 /* Message of the last failed call on this thread ("" if none). */
 H3A_API const char *h3a_last_error(void);
 

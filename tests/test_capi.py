@@ -38,6 +38,7 @@ def test_header_declares_the_expected_entry_points():
         "h3a_attn_fwd_noalloc",
         "h3a_attn_fwd_workspace_size",
         "h3a_attn_merge",
+        "h3a_clock_sample",
         "h3a_last_error",
         "h3a_merge_heads",
         "h3a_pack_qkv",
@@ -58,6 +59,13 @@ def test_library_exports_every_declared_function(lib):
 
 def test_abi_version(lib):
     assert lib.h3a_abi_version() == _ext.ABI_VERSION == 4
+
+
+def test_clock_sample_rejects_bad_pointers(lib):
+    assert lib.h3a_clock_sample(None, None) == _ext.H3A_EINVAL
+    assert b"NULL" in lib.h3a_last_error()
+    assert lib.h3a_clock_sample(ctypes.c_void_p((1 << 20) + 4), None) == _ext.H3A_EINVAL
+    assert b"aligned" in lib.h3a_last_error()
 
 
 def _attn_args(**overrides):
