@@ -90,6 +90,14 @@ extern "C" {
  *
  * Rows with no key (seqlen_k == 0) produce O = 0 and LSE = -inf.
  *
+ * Strides: non-negative multiples of 8 elements, the sequence stride at least
+ * head_dim. A (batch, head) view may be of any length (strided views of a
+ * packed to_qkv output included), but 576 of its rows must span less than
+ * 2^31 bytes: a sequence stride under 1,864,136 elements; larger strides
+ * return H3A_EUNSUPPORTED. Views whose rows plus an 896-row margin reach
+ * 2^31 bytes run in a form of the kernel that rebases its buffer resources
+ * per query tile and per 576-row window of keys.
+ *
  * Workspace: h3a_attn_fwd_workspace_size(args) bytes of device memory at
  * `workspace` (256-byte aligned, contents on entry irrelevant), used for:
  *   - the split tail: with more query tiles (256 rows of one head) than the

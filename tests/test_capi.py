@@ -132,6 +132,19 @@ def test_attn_null_args_and_empty_problem(lib):
     assert _ext.last_error(lib) == ""
 
 
+def test_row_stride_limit_is_one_window_of_rows(lib):
+    # 576 rows of a view must span under 2^31 bytes: 1,864,135 elements is
+    # the largest sequence stride (1,864,128 the largest multiple of 8)
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        ok = _attn_args()
+        getattr(ok, name)[:] = (0, 1_864_128, 128)
+        assert lib.h3a_attn_fwd_workspace_size(ctypes.byref(ok)) >= 0, name
+        bad = _attn_args()
+        getattr(bad, name)[:] = (0, 1_864_136, 128)
+        assert lib.h3a_attn_fwd_workspace_size(ctypes.byref(bad)) == _ext.H3A_EUNSUPPORTED, name
+        assert "2^31" in _ext.last_error(lib)
+
+
 def test_workspace_size_validates_like_the_launch(lib):
     # host-only call: no device work whether or not a GPU is visible
     assert lib.h3a_attn_fwd_workspace_size(None) == _ext.H3A_EINVAL
