@@ -295,8 +295,8 @@ class _H3Attention:
 
 def block_rates(torch, heads: int = 40, head_dim: int = 128, grid=(32, 30, 52)) -> dict:
     """One H3 attention block (projections, q/k RMSNorm + 3D RoPE, attention,
-    out-projection) through the HIP processor (also with the projections
-    unfused, and with the out-projection fused too), against the reference's eager
+    out-projection) through the HIP processor (also with q/k/v through the
+    fused projection GEMM, and with the out-projection fused too), against the reference's eager
     composition on the same GPU (dense_fa4.py:123-140,169-170 with torch SDPA
     as at packed_ulysses.py:202-209)."""
 
@@ -326,15 +326,15 @@ def block_rates(torch, heads: int = 40, head_dim: int = 128, grid=(32, 30, 52)) 
         o = functional.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
         return attn.to_out[0](o.transpose(1, 2).flatten(2, 3))
 
-    unfused = DenseMiniMaxH3Processor(fuse_projections=False)
-    all_fused = DenseMiniMaxH3Processor(fuse_out_projection=True)
+    fused = DenseMiniMaxH3Processor(fuse_projections=True)
+    all_fused = DenseMiniMaxH3Processor(fuse_projections=True, fuse_out_projection=True)
 
     def ours():
         return processor(attn, x, (cos, sin))
 
     with torch.no_grad():
         ours_ms = _time_ms(torch, ours, reps=5)
-        unfused_ms = _time_ms(torch, lambda: unfused(attn, x, (cos, sin)), reps=5)
+        fused_ms = _time_ms(torch, lambda: fused(attn, x, (cos, sin)), reps=5)
         all_fused_ms = _time_ms(torch, lambda: all_fused(attn, x, (cos, sin)), reps=5)
         eager_ms = _time_ms(torch, eager, reps=3)
     attn_flop = 4.0 * S * S * head_dim * heads
@@ -342,11 +342,12 @@ def block_rates(torch, heads: int = 40, head_dim: int = 128, grid=(32, 30, 52)) 
     return {
         "workload": f"one H3 attention block: B=1 S={S} heads={heads} head_dim={head_dim} hidden={heads * head_dim}, "
         "random-init weights, bf16",
-        # the processor as installed: q/k/v through the fused projection GEMM,
-        # the out-projection on hipBLASLt
+        # the processor as installed: every projection on hipBLASLt, then the
+        # HIP q/k prologue (the reference's rounding order)
         "hip_processor_ms": ours_ms,
-        # every projection on hipBLASLt, then the HIP q/k prologue
-        "hip_processor_unfused_projections_ms": unfused_ms,
+        # q/k/v through the fused projection GEMM (norm + RoPE in its
+        # epilogue), the out-projection on hipBLASLt
+        "hip_processor_fused_projections_ms": fused_ms,
         # the out-projection through the projection GEMM too
         "hip_processor_fused_out_projection_ms": all_fused_ms,
         "eager_torch_sdpa_ms": eager_ms,

@@ -295,16 +295,21 @@ class DenseMiniMaxH3Processor:
         self,
         *,
         kernel: Callable[..., Any] | None = None,
-        fuse_projections: bool = True,
+        fuse_projections: bool = False,
         fuse_out_projection: bool = False,
     ) -> None:
         self.kernel = load_kernel() if kernel is None else kernel
         self.calls = 0
         # fuse_projections: q/k/v come from one h3a_proj_gemm launch with the
         # q/k RMSNorm + RoPE in its epilogue (modules or inputs outside what
-        # it takes keep the separate steps). fuse_out_projection: to_out[0]
-        # runs on h3a_proj_gemm too; off by default, hipBLASLt's GEMM is 1-4%
-        # faster there and there is no epilogue to fold.
+        # it takes keep the separate steps). Off by default: the module's
+        # projections (hipBLASLt) followed by the HIP prologue keep the
+        # reference's rounding order (projection rounded to bf16, then norm
+        # and RoPE) and measured as fast or faster than the fused launch,
+        # whose epilogue runs while the CU's matrix cores idle.
+        # fuse_out_projection: to_out[0] runs on h3a_proj_gemm too; off by
+        # default, hipBLASLt's GEMM is 1-4% faster there and there is no
+        # epilogue to fold.
         self.fuse_projections = fuse_projections
         self.fuse_out_projection = fuse_out_projection
         # Set by install_dense_hip on the first module: the install record,
@@ -375,7 +380,7 @@ def install_dense_hip(
     transformer: Any,
     attention_class: type | None = None,
     *,
-    fuse_projections: bool = True,
+    fuse_projections: bool = False,
     fuse_out_projection: bool = False,
 ) -> dict[str, Any]:
     """Install one shared HIP kernel on every H3 attention module.

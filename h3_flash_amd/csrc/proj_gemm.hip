@@ -2,10 +2,12 @@
 // prologue as its epilogue (gfx950).
 //
 //   y[m, f] = sum_k x[m, k] * w[f, k] (+ bias[f])            (nn.Linear)
-//   q / k sections: per (token m, head of 128 features) the fp32 result is
-//   RMS-normalised, scaled by the norm weight and rotated (rotate-half RoPE
-//   over the first R features, table row m mod seqlen), then rounded once
-//   to bf16; v and out-projection sections are stored as they are.
+//   q / k sections: per (token m, head of 128 features) the result, rounded
+//   to bf16 as the module's linear outputs it, is RMS-normalised in fp32,
+//   scaled by the norm weight and rotated (rotate-half RoPE over the first R
+//   features, table row m mod seqlen), then rounded to bf16 again: the
+//   reference's order of a projection followed by fused_qknorm_rope; v and
+//   out-projection sections are stored as they are.
 //
 // x (M tokens x K) and w (N features x K) are bf16 with K contiguous (the
 // nn.Linear layout). The product is computed transposed, C^T = W X^T, on
@@ -151,7 +153,7 @@ static_assert(kPSmem <= 160 * 1024, "LDS of one workgroup");
 __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoord& tc, const f32x4 (&acc)[8][8],
                                          int wave, int wn, int wm, int lane, char* smem) {
     // Opaque here, so that no lane-derived value of the epilogue is hoisted
-    // out of the tile loop and held (or spilled) across the K loop.
+    // and held (or spilled) across the K loop.
     asm volatile("" : "+v"(lane));
     const ProjSection sec = section(p, tc.sec);
     // Lane l holds, for token block b (token wm*128 + 16b + (l & 15)) and
@@ -204,13 +206,26 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
     }
 
     // bias, then RMSNorm over the head (sum of squares in-lane, then over
-    // lanes l ^ 16 and l ^ 32) and the norm weight.
+    // lanes l ^ 16 and l ^ 32) and the norm weight. Norm sections first round
+    // the projection to bf16, as the module's linear outputs it, so the norm
+    // and RoPE see the values the reference's separate steps see
+    // (dense_fa4.py:123-140, transformer.py:146-173); rounding only once, at
+    // the end, moves the LSE of the attention that follows by up to about
+    // 2e-3 against that order.
     auto normed = [&](int b, float (&v)[8][4], auto norm_c) __attribute__((always_inline)) {
 #pragma unroll
         for (int a = 0; a < 8; ++a)
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[a][e] = acc[a][b][e] + bias[a][e];
         if constexpr (decltype(norm_c)::value) {
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                    const uint32_t r = pack_bf16x2(v[a][e], v[a][e + 1]);
+                    v[a][e] = __uint_as_float(r << 16);
+                    v[a][e + 1] = __uint_as_float(r & 0xffff0000u);
+                }
             // Four partial sums (over e), added at the end: short dependency
             // chains for a lone wave.
             float s4[4] = {0.f, 0.f, 0.f, 0.f};
@@ -351,19 +366,20 @@ __global__ __launch_bounds__(kPThreads, 1) void proj_gemm_kernel(ProjGemmParams 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave >> 1, wm = wave & 1;
 
-    // Persistent workgroups. Workgroup b runs on XCD b mod 8 (round-robin
-    // dispatch); each XCD owns one contiguous range of tiles, and its
-    // workgroups take the range's tiles in turn, so the ~32 tiles an XCD runs
-    // at a time are consecutive in the grouped order (about 2 token tiles x
-    // 16 feature tiles sharing their X and W panels in the XCD's L2).
+    // One workgroup per tile. Workgroup b runs on XCD b mod 8 (round-robin
+    // dispatch) as that XCD's (b / 8)-th; each XCD owns one contiguous range
+    // of the grouped tile order, so the ~32 tiles an XCD runs at a time are
+    // consecutive in it (about 2 token tiles x 16 feature tiles sharing their
+    // X and W panels in the XCD's L2). (A persistent grid of one workgroup
+    // per CU looping over its XCD's range measured from 1% faster to 4%
+    // slower, and is not used.)
     const int total = p.m_tiles * p.n_tiles;
-    const int G = gridDim.x, bid = blockIdx.x;
+    const int bid = blockIdx.x;
     const int xcd = bid & 7, local = bid >> 3;
     const int per = total >> 3, rem = total & 7;
     const int first = xcd * per + min(xcd, rem), end = first + per + (xcd < rem ? 1 : 0);
-    const int stride = (G >> 3) + (xcd < (G & 7) ? 1 : 0);  // workgroups on this XCD
-    int tile = first + local;
-    if (tile >= end) return;
+    const int tile = first + local;
+    if (tile >= end) return;  // the grid is the tile count: never taken
 
     // DMA map: load i of a wave fills rows (8*wave + i)*8 .. +8 of an operand
     // tile; lane L writes LDS chunk (L & 7) of row r0 + (L >> 3), which holds
@@ -464,11 +480,10 @@ __global__ __launch_bounds__(kPThreads, 1) void proj_gemm_kernel(ProjGemmParams 
         }
     };
 
-    for (;;) {
+    {
         const TileCoord tc = tile_coord(p, tile);
         const TileSrc cur = source(tc);
-        // The tile's first two K steps (the stage memory is free: first tile,
-        // or every wave is past the previous tile's store phase).
+        // The tile's first two K steps.
 #pragma unroll
         for (int j = 0; j < 16; ++j) dma_src(cur, 0, 0, j);
 #pragma unroll
@@ -526,12 +541,6 @@ __global__ __launch_bounds__(kPThreads, 1) void proj_gemm_kernel(ProjGemmParams 
         // the last ones time to write their results before they are read.
         asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
         epilogue(p, tc, acc, wave, wn, wm, lane, smem);
-        // Every wave's table reads are done before the next tile's loads
-        // overwrite the stage memory.
-        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
-        barrier();
-        tile += stride;
-        if (tile >= end) return;
     }
 }
 

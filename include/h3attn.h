@@ -441,15 +441,17 @@ H3A_API int h3a_attn_merge(const h3a_attn_merge_args *args, void *stream);
  * and then per section mode:
  *   H3A_PROJ_PLAIN:        y[m, f] = bf16(acc)
  *   H3A_PROJ_QKNORM_ROPE:  per head (128 consecutive features) of token m,
- *     n = acc * rsqrt(sum(acc^2) / 128 + eps) * norm_weight[f mod 128], then
+ *     with p = bf16(acc) (the projection as the module's linear outputs it),
+ *     n = p * rsqrt(sum(p^2) / 128 + eps) * norm_weight[f mod 128], then
  *     rotate-half RoPE over the head's first rotary_dim features with table
  *     row s = m mod seqlen:
  *       y[c] = n[c] cos[s,c] - n[c+R/2] sin[s,c]   (c < R/2)
  *       y[c] = n[c] cos[s,c] + n[c-R/2] sin[s,c]   (R/2 <= c < R)
  *       y[c] = n[c]                                (c >= R)
- *     stored once as bf16 (rotary_dim 0: the norm alone).
+ *     in fp32, stored as bf16 (rotary_dim 0: the norm alone).
  * This is the reference's projection step followed by its fused q/k norm +
- * RoPE without the intermediate bf16 rounding of the projection output:
+ * RoPE, in the reference's rounding order (the projection rounded to bf16,
+ * then the norm and RoPE computed in fp32 and rounded once more):
  *   attn.to_qkv(hidden_states).chunk(3) or to_q / to_k / to_v
  *     (src/h3_flash/runtime/attention/dense_fa4.py:123-128,
  *      src/h3_flash/runtime/kernels/transformer.py:146-152),

@@ -12,10 +12,11 @@ The reference computes, per token row of ``hidden_states``:
   (transformer.py:160-173; src/h3_flash/runtime/kernels/fusions.py:126-175,
   268-293), restated in :func:`oracle.qknorm_rope.qknorm_rope_reference`.
 
-The fused launch this checks feeds the fp32 projection straight into the
-norm (one bf16 rounding of q and k, at the end); the reference rounds the
-projection to bf16 first. ``round_projection=True`` gives the reference's
-order, so tests can bound the difference between the two.
+The reference rounds the projection to bf16 (the linear's output dtype)
+before the norm; ``round_projection=True``, the default, follows that order,
+as the fused launch does. ``round_projection=False`` feeds the fp32 product
+straight into the norm (one bf16 rounding of q and k, at the end), so tests
+can bound the difference between the two orders.
 """
 
 from __future__ import annotations
@@ -37,15 +38,16 @@ def projection_reference(
     sin: torch.Tensor | None = None,
     seqlen: int | None = None,
     head_dim: int = 128,
-    round_projection: bool = False,
+    round_projection: bool = True,
 ) -> torch.Tensor:
     """(m, k) x (n, k) -> (m, n) bf16.
 
     Without ``norm_weight``: ``bf16(x @ W^T + b)`` from an fp32 product.
-    With it: each head of ``head_dim`` features of the fp32 product is
-    normalised, weighted and rotated (tables ``cos``/``sin`` of ``seqlen``
-    rows, token row ``i`` using row ``i % seqlen``; no tables: the norm
-    alone), then rounded once.
+    With it: each head of ``head_dim`` features of the product (rounded to
+    bf16 first when ``round_projection``) is normalised, weighted and
+    rotated in fp32 (tables ``cos``/``sin`` of ``seqlen`` rows, token row
+    ``i`` using row ``i % seqlen``; no tables: the norm alone), then rounded
+    to bf16.
     """
 
     xf = x.detach().to("cpu", torch.float32)

@@ -32,17 +32,29 @@ def tables(seqlen: int, R: int, seed: int = 0):
     return theta.cos().contiguous(), theta.sin().contiguous()
 
 
-def assert_matches(got: torch.Tensor, ref: torch.Tensor, what: str = ""):
+def assert_matches(got: torch.Tensor, ref: torch.Tensor, what: str = "", rounded_projection: bool = False):
     """Within one bf16 step of the oracle's value plus 2^-9 of the row's RMS
     (the two sides sum the K products in different orders, and a value that
-    nearly cancels keeps that absolute error), and mostly bit-identical."""
+    nearly cancels keeps that absolute error), and mostly bit-identical.
+
+    ``rounded_projection`` (q and k: the projection is rounded to bf16 before
+    the norm): where the two summation orders put a projection value on two
+    sides of a bf16 rounding boundary, the normalised value moves by up to
+    2^-7 of itself, and both outputs its rotation feeds move with it. Those
+    elements (rare) may differ by up to 2^-4 of the row's RMS."""
 
     got, ref = got.float().cpu(), ref.float()
     d = (got - ref).abs()
     ulp = 2.0 ** (torch.floor(torch.log2(ref.abs().clamp_min(1e-30))) - 7)
     rms = ref.pow(2).mean(dim=1, keepdim=True).sqrt()
-    bad = d > ulp + rms * 2.0**-9
-    assert not bad.any(), (what, int(bad.sum()), float((d / (ulp + rms * 2.0**-9)).max()))
+    tight = ulp + rms * 2.0**-9
+    bad = d > tight
+    if rounded_projection:
+        loose = ulp + rms * 2.0**-4
+        assert not (d > loose).any(), (what, int((d > loose).sum()), float((d / loose).max()))
+        assert bad.float().mean() <= 5e-3, (what, int(bad.sum()))
+    else:
+        assert not bad.any(), (what, int(bad.sum()), float((d / tight).max()))
     assert (d == 0).float().mean() > 0.99, (what, float((d == 0).float().mean()))
 
 
@@ -82,8 +94,8 @@ def check_qkv(x, w, b, nwq, nwk, cos, sin, seqlen, y, rows=None, eps=1e-6):
         idx = torch.as_tensor(rows) % seqlen
         cos, sin, seqlen = cos[idx], sin[idx], len(rows)
     bb = (lambda i: None) if b is None else (lambda i: b[i * n : (i + 1) * n])
-    assert_matches(ys[:, :n], projection_reference(xs, w[:n], bb(0), nwq, eps, cos, sin, seqlen), "q")
-    assert_matches(ys[:, n : 2 * n], projection_reference(xs, w[n : 2 * n], bb(1), nwk, eps, cos, sin, seqlen), "k")
+    assert_matches(ys[:, :n], projection_reference(xs, w[:n], bb(0), nwq, eps, cos, sin, seqlen), "q", True)
+    assert_matches(ys[:, n : 2 * n], projection_reference(xs, w[n : 2 * n], bb(1), nwk, eps, cos, sin, seqlen), "k", True)
     assert_matches(ys[:, 2 * n :], projection_reference(xs, w[2 * n :], bb(2)), "v")
 
 

@@ -15,8 +15,9 @@ from oracle.projection import projection_reference
 from oracle.qknorm_rope import qknorm_rope_reference
 
 
-def brute_fp64(x, w, b, nw, eps, cos, sin, seqlen, head_dim=128):
-    """Loops in float64: product, bias, per-head RMSNorm, weight, rotate-half."""
+def brute_fp64(x, w, b, nw, eps, cos, sin, seqlen, head_dim=128, round_projection=True):
+    """Loops in float64: product, bias, (the projection rounded to bf16, as
+    the linear outputs it), per-head RMSNorm, weight, rotate-half."""
 
     x, w = x.double().numpy(), w.double().numpy()
     m, n = x.shape[0], w.shape[0]
@@ -26,6 +27,8 @@ def brute_fp64(x, w, b, nw, eps, cos, sin, seqlen, head_dim=128):
             acc[i, f] = float(np.dot(x[i], w[f])) + (float(b[f]) if b is not None else 0.0)
     if nw is None:
         return acc
+    if round_projection:
+        acc = torch.from_numpy(acc).to(torch.bfloat16).double().numpy()
     nw = nw.double().numpy()
     R = 0 if cos is None else cos.shape[1]
     out = np.zeros_like(acc)
@@ -75,10 +78,20 @@ def assert_within_one_ulp(got: torch.Tensor, exact: np.ndarray):
 
 
 @pytest.mark.parametrize("R, seqlen, bias", [(64, 3, True), (128, 5, False), (0, 1, True), (32, 2, True)])
-def test_matches_float64_brute_force(R, seqlen, bias):
+@pytest.mark.parametrize("round_projection", [True, False])
+def test_matches_float64_brute_force(R, seqlen, bias, round_projection):
     x, w, b, nw, cos, sin = case(R=R, seqlen=seqlen, bias=bias)
-    got = projection_reference(x, w, b, nw, 1e-6, cos, sin, seqlen)
-    assert_within_one_ulp(got, brute_fp64(x, w, b, nw, 1e-6, cos, sin, seqlen))
+    got = projection_reference(x, w, b, nw, 1e-6, cos, sin, seqlen, round_projection=round_projection)
+    assert_within_one_ulp(got, brute_fp64(x, w, b, nw, 1e-6, cos, sin, seqlen, round_projection=round_projection))
+
+
+def test_default_order_is_the_rounded_projection():
+    # the default follows the reference: bf16 projection, then the prologue
+    # oracle on it (transformer.py:146-173)
+    x, w, b, nw, cos, sin = case(m=9, k=64, heads=2, R=64, seqlen=9, seed=3)
+    proj = torch.nn.functional.linear(x.float(), w.float(), b.float()).to(torch.bfloat16)
+    want = qknorm_rope_reference(proj.view(1, 9, 2, 128), nw, cos, sin, 1e-6).view(9, 256)
+    assert torch.equal(projection_reference(x, w, b, nw, 1e-6, cos, sin, 9), want)
 
 
 def test_plain_section_is_an_fp32_linear():
@@ -114,7 +127,7 @@ def test_single_rounding_differs_from_the_rounded_projection_by_the_projection_r
     # at most one bf16 step of the largest outputs (2^-4 at |y| < 8), 2^-8 on
     # average, on a minority of elements
     x, w, b, nw, cos, sin = case(m=64, k=256, R=128, seqlen=64, seed=4)
-    once = projection_reference(x, w, b, nw, 1e-6, cos, sin, 64).float()
+    once = projection_reference(x, w, b, nw, 1e-6, cos, sin, 64, round_projection=False).float()
     twice = projection_reference(x, w, b, nw, 1e-6, cos, sin, 64, round_projection=True).float()
     d = (once - twice).abs()
     assert 0 < (once != twice).float().mean() < 0.5
