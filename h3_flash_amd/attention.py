@@ -316,6 +316,10 @@ class DenseMiniMaxH3Processor:
         # whose "gate" receives the fused prologue's error on the first call
         # (transformer.py:174-190).
         self._runtime: dict[str, Any] | None = None
+        # Set by install_dense_hip on every module: the same record, whose
+        # "projection_fallbacks" counts, per reason, the calls in which
+        # fuse_projections was asked for and the separate steps ran.
+        self._audit: dict[str, Any] | None = None
 
     def __call__(
         self,
@@ -330,7 +334,14 @@ class DenseMiniMaxH3Processor:
             raise RuntimeError(
                 "dense HIP attention runs one GPU's head shard; context parallelism is not installed"
             )
-        fused = qkv_projection(attn, hidden_states, rotary_emb) if self.fuse_projections else None
+        fused = None
+        if self.fuse_projections:
+            why: list[str] = []
+            fused = qkv_projection(attn, hidden_states, rotary_emb, why)
+            if fused is None and self._audit is not None:
+                counts = self._audit.setdefault("projection_fallbacks", {})
+                for reason in why:
+                    counts[reason] = counts.get(reason, 0) + 1
         if fused is not None:
             query, key, value = fused
             if self._runtime is not None and "qknorm_partial_rope" not in self._runtime["gate"]:
@@ -393,7 +404,10 @@ def install_dense_hip(
     The returned record is live: its ``"gate"`` dict receives, on the first
     rotary call of the first module, the error metrics of the fused q/k
     RMSNorm + RoPE against the eager composition, as the reference's fused
-    runtime records them (transformer.py:174-190).
+    runtime records them (transformer.py:174-190); with
+    ``fuse_projections``, its ``"projection_fallbacks"`` dict counts, per
+    reason, the calls of any module that ran the separate projection steps
+    instead of the fused projection GEMM.
     """
 
     kernel = load_kernel()
@@ -419,7 +433,11 @@ def install_dense_hip(
         "semantics": "dense",
         "processor_count": len(processors),
         **provenance(),
+        "fuse_projections": bool(fuse_projections),
         "gate": {},
+        "projection_fallbacks": {},
     }
     processors[0]._runtime = record
+    for processor in processors:
+        processor._audit = record
     return record

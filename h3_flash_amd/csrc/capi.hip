@@ -571,11 +571,9 @@ int h3a_qknorm_rope_pack(const h3a_qknorm_rope_pack_args* a, void* stream) {
     p.div_tensors = h3a::make_fast_div(2u);
     p.div_seqlen = h3a::make_fast_div((uint32_t)a->rows);
     p.div_hpg = h3a::make_fast_div((uint32_t)hl);
-    if (!h3a::qknorm_rope_fast_path(p))
-        return fail(H3A_EUNSUPPORTED,
-                    "h3a_qknorm_rope_pack: rotary_dim %lld needs a multiple of 16 and 16-byte aligned cos/sin rows; "
-                    "use h3a_qknorm_rope then h3a_pack_qkv",
-                    (long long)R);
+    // Rotary widths that are not a multiple of 16, or tables without 16-byte
+    // rows, take the generic kernel (one row per lane group, element-wise
+    // partner and table reads) in the same output layout.
     hipError_t e = h3a::launch_qknorm_rope(p, (hipStream_t)stream);
     if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_qknorm_rope_pack: launch failed: %s", hipGetErrorString(e));
     return H3A_OK;
@@ -782,29 +780,25 @@ int h3a_proj_gemm(const h3a_proj_args* a, void* stream) {
         d.eps = s.eps;
         n_tiles += d.tiles;
     }
-    if (any_norm && R % 32 != 0)
-        return fail(H3A_EUNSUPPORTED,
-                    "%s: rotary_dim %lld: the fused epilogue takes multiples of 32 (0, 32, 64, 96, 128); use a plain "
-                    "projection and h3a_qknorm_rope",
-                    fn, (long long)R);
-    if (any_norm && R > 0 && a->rotate_half_tables != 1)
-        return fail(H3A_EUNSUPPORTED,
-                    "%s: the fused epilogue reads rotate-half tables (columns c and c + rotary_dim/2 equal, "
-                    "rotate_half_tables = 1); use a plain projection and h3a_qknorm_rope",
-                    fn);
     if (any_norm && R > 0) {
         if (!a->cos || !a->sin) return fail(H3A_EINVAL, "%s: NULL cos/sin table", fn);
         if (a->seqlen <= 0 || a->seqlen >= ((int64_t)1 << 31)) return fail(H3A_EINVAL, "%s: seqlen must be in [1, 2^31)", fn);
         if (a->table_stride < R) return fail(H3A_EINVAL, "%s: table_stride < rotary_dim", fn);
         if (a->table_stride > span_limit / 4 / a->seqlen)
             return fail(H3A_EUNSUPPORTED, "%s: cos/sin tables must span less than 2^32 bytes", fn);
-        if (!aligned16(a->cos) || !aligned16(a->sin) || a->table_stride % 4 != 0)
-            return fail(H3A_EINVAL, "%s: cos/sin must be 16-byte aligned with table_stride a multiple of 4", fn);
+        if (!aligned4(a->cos) || !aligned4(a->sin)) return fail(H3A_EINVAL, "%s: cos/sin must be 4-byte aligned", fn);
         p.cos = a->cos;
         p.sin = a->sin;
         p.table_stride = a->table_stride;
         p.rotary_dim = (int32_t)R;
         p.seqlen = (int32_t)a->seqlen;
+        // The in-lane epilogue (partners in the same lane, only the first
+        // half of the tables read) needs R a multiple of 32, the caller's
+        // word that the tables are in the rotate-half form, and 16-byte
+        // table rows; anything else reads the tables at every column.
+        const bool in_lane = R % 32 == 0 && a->rotate_half_tables == 1 && aligned16(a->cos) && aligned16(a->sin) &&
+                             a->table_stride % 4 == 0;
+        p.rope_full_tables = in_lane ? 0 : 1;
     } else {
         p.rotary_dim = 0;
         p.seqlen = 1;

@@ -139,12 +139,12 @@ struct QkNormRopeParams {
     int32_t head_dim;
     int32_t rotary_dim;
     int32_t w_f32;  // 1: weights are fp32, 0: bf16
-    // Grouped output heads (fast path only): head h of y is stored at
+    // Grouped output heads: head h of y is stored at
     // (h / hpg) * y_sg + (h % hpg) * y_sh; hpg == heads means ungrouped.
     FastDiv div_hpg;
     int64_t y_sg[2];
     // Optional third tensor copied verbatim (no arithmetic) into the same
-    // grouped layout (fast path only; NULL: none).
+    // grouped layout (NULL: none).
     const void* xc;
     void* yc;
     int64_t xc_sb, xc_ss, xc_sh;
@@ -256,6 +256,11 @@ struct ProjGemmParams {
     int32_t rotary_dim;
     int32_t seqlen;  // token m uses table row m % seqlen
     int32_t stage_plain;  // 1: sections without RoPE stage their rows in LDS like the RoPE sections
+    // 1: the RoPE epilogue reads cos / sin at every rotated column and takes
+    // the partners from the token's other lanes (any even rotary_dim, tables
+    // in any form, 4-byte aligned); 0: rotary_dim a multiple of 32 with
+    // rotate-half tables, 16-byte aligned, read at their first half only.
+    int32_t rope_full_tables;
 };
 int proj_gemm_tile();
 int proj_gemm_k_multiple();  // k must be a multiple of this

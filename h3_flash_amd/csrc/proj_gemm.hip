@@ -134,7 +134,10 @@ struct TileSrc {
 // c of row r at c ^ (r mod 32), so that the 16 rows of a quarter-wave's
 // writes fall in distinct bank pairs.
 constexpr int kPOutWave = 128 * 256;
-constexpr int kPSmem = kPLds;
+// RoPE epilogue with partners in other lanes: per wave, one token block's
+// bf16 projection rows (16 tokens x 256 bytes), past the stage memory.
+constexpr int kPRowsWave = 16 * 256;
+constexpr int kPSmem = kPLds + kPWaves * kPRowsWave;
 static_assert(kPWaves * kPOutWave <= kPLds, "output rows fit the stage memory");
 static_assert(kPSmem <= 160 * 1024, "LDS of one workgroup");
 
@@ -328,16 +331,98 @@ __device__ __forceinline__ void epilogue(const ProjGemmParams& p, const TileCoor
             }
         }
     };
+    // Any other even R, or tables read at every rotated column: the partner
+    // c +- R/2 of feature c is in general held by another lane of the token,
+    // at another position. The norm starts from the bf16-rounded projection,
+    // so the token's projection row is exact in bf16: it goes into the
+    // wave's LDS row of the token (feature f at byte 2f, past the stage
+    // memory), each lane reads its partners' values back, normalises them
+    // with the token's r (the same in the 4 lanes of a token) and the
+    // partner's norm weight, and reads cos / sin at its own columns. A
+    // wave's LDS operations run in order: every lane's row writes precede
+    // the reads, and a block's reads precede the next block's writes (the
+    // memory clobbers keep the compiler from moving one past the other).
+    lds_char* const prows = (lds_char*)smem + kPLds + wave * kPRowsWave;
+    auto cross_lane = [&]() __attribute__((always_inline)) {
+        const int rh = R >> 1;
+        float wpart[8][4];  // norm weight at the partner column
+#pragma unroll
+        for (int a = 0; a < 8; ++a)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int c = 16 * a + fl + e;
+                const int pc = c < rh ? c + rh : c - rh;
+                wpart[a][e] = c < R ? bf16_to_f32(((const uint16_t*)sec.norm_w)[pc]) : 0.f;
+            }
+        // (Unrolled: the accumulators are registers, indexed by constants.)
+#pragma unroll
+        for (int b = 0; b < 8; ++b) {
+            float v[8][4];
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+#pragma unroll
+                for (int e = 0; e < 4; e += 2) {
+                    const uint32_t h2 = pack_bf16x2(acc[a][b][e] + bias[a][e], acc[a][b][e + 1] + bias[a][e + 1]);
+                    v[a][e] = __uint_as_float(h2 << 16);
+                    v[a][e + 1] = __uint_as_float(h2 & 0xffff0000u);
+                }
+            const int r = 16 * b + j16;
+            lds_char* const prow = prows + j16 * 256;
+            asm volatile("" ::: "memory");
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+                *(__attribute__((address_space(3))) i32x2*)(prow + (16 * a + fl) * 2) =
+                    i32x2{(int)pack_bf16x2(v[a][0], v[a][1]), (int)pack_bf16x2(v[a][2], v[a][3])};
+            asm volatile("" ::: "memory");
+            float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int a = 0; a < 8; ++a)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) s4[e] += v[a][e] * v[a][e];
+            float ss = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+            auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(ss), __float_as_uint(ss), false, false);
+            ss = __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+            const f32x2 hs = halves(ss);
+            ss = hs[0] + hs[1];
+            const float rn = rsqrtf(ss * (1.0f / 128.0f) + sec.eps);
+            int tok = m_head + r;
+            tok = tok < seqlen ? tok : tok % seqlen;
+            const uint32_t trow = (uint32_t)tok * row_bytes;
+#pragma unroll
+            for (int a = 0; a < 8; ++a) {
+                float y[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int c = 16 * a + fl + e;
+                    const float n = (v[a][e] * rn) * nw[a][e];
+                    y[e] = n;
+                    if (c < R) {
+                        const int pc = c < rh ? c + rh : c - rh;
+                        const float pp = bf16_to_f32(*(const __attribute__((address_space(3))) uint16_t*)(prow + pc * 2));
+                        const float pn = (pp * rn) * wpart[a][e];
+                        const uint32_t to = trow + (uint32_t)c * 4u;
+                        const float cv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rcos, (int)to, 0, 0));
+                        const float sv = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rsin, (int)to, 0, 0));
+                        y[e] = n * cv + (c < rh ? -pn : pn) * sv;
+                    }
+                }
+                const i32x2 w{(int)pack_bf16x2(y[0], y[1]), (int)pack_bf16x2(y[2], y[3])};
+                *(__attribute__((address_space(3))) i32x2*)(orow + r * 256 + ((((4 * a + (lane >> 4)) ^ r) & 31) << 3)) = w;
+            }
+        }
+    };
     using Y = std::true_type;
     if (!norm) {
         in_lane(std::integral_constant<int, 0>{}, std::false_type{});
+    } else if (R > 0 && p.rope_full_tables != 0) {
+        cross_lane();
     } else {
         switch (R) {
             case 0: in_lane(std::integral_constant<int, 0>{}, Y{}); break;
             case 32: in_lane(std::integral_constant<int, 1>{}, Y{}); break;
             case 64: in_lane(std::integral_constant<int, 2>{}, Y{}); break;
             case 96: in_lane(std::integral_constant<int, 3>{}, Y{}); break;
-            default: in_lane(std::integral_constant<int, 4>{}, Y{}); break;  // 128 (the caller admits multiples of 32)
+            default: in_lane(std::integral_constant<int, 4>{}, Y{}); break;  // 128 (other widths: cross_lane)
         }
     }
     if (!active || !staged) return;  // the rows went out directly

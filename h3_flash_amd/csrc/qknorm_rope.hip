@@ -68,7 +68,7 @@ __device__ __forceinline__ int64_t head_ofs(const QkNormRopeParams& p, int h, in
 struct RowRef {
     const uint16_t* x;
     uint16_t* y;
-    uint32_t s;
+    uint32_t s, h, b;
     int which;
     bool ok;
 };
@@ -78,16 +78,17 @@ __device__ __forceinline__ RowRef locate(const QkNormRopeParams& p, uint32_t row
     r.ok = row < (uint32_t)p.rows;
     const uint32_t rr = r.ok ? row : 0u;
     const uint32_t t = fdiv(rr, p.div_heads);
-    const uint32_t h = rr - t * p.div_heads.d;
+    r.h = rr - t * p.div_heads.d;
     const uint32_t t2 = fdiv(t, p.div_tensors);
     r.which = (int)(t - t2 * p.div_tensors.d);
-    const uint32_t b = fdiv(t2, p.div_seqlen);
-    r.s = t2 - b * p.div_seqlen.d;
+    r.b = fdiv(t2, p.div_seqlen);
+    r.s = t2 - r.b * p.div_seqlen.d;
     const bool second = r.which != 0;
-    r.x = (const uint16_t*)(second ? p.x[1] : p.x[0]) + (int64_t)b * (second ? p.x_sb[1] : p.x_sb[0]) +
-          (int64_t)r.s * (second ? p.x_ss[1] : p.x_ss[0]) + (int64_t)h * (second ? p.x_sh[1] : p.x_sh[0]);
-    r.y = (uint16_t*)(second ? p.y[1] : p.y[0]) + (int64_t)b * (second ? p.y_sb[1] : p.y_sb[0]) +
-          (int64_t)r.s * (second ? p.y_ss[1] : p.y_ss[0]) + (int64_t)h * (second ? p.y_sh[1] : p.y_sh[0]);
+    r.x = (const uint16_t*)(second ? p.x[1] : p.x[0]) + (int64_t)r.b * (second ? p.x_sb[1] : p.x_sb[0]) +
+          (int64_t)r.s * (second ? p.x_ss[1] : p.x_ss[0]) + (int64_t)r.h * (second ? p.x_sh[1] : p.x_sh[0]);
+    r.y = (uint16_t*)(second ? p.y[1] : p.y[0]) + (int64_t)r.b * (second ? p.y_sb[1] : p.y_sb[0]) +
+          (int64_t)r.s * (second ? p.y_ss[1] : p.y_ss[0]) +
+          head_ofs(p, (int)r.h, second ? p.y_sh[1] : p.y_sh[0], second ? p.y_sg[1] : p.y_sg[0]);
     return r;
 }
 
@@ -251,7 +252,9 @@ __global__ __launch_bounds__(kThreads, kCopy ? 3 : 4) void qknorm_rope_kernel(Qk
 }
 
 // Generic path (any even R <= D, any table alignment): one row per lane
-// group, element-wise partner and table reads.
+// group, element-wise partner and table reads. Output heads may be grouped
+// (the pack layout), and a copied third tensor goes along with the first
+// tensor's rows (each (batch, token, head) once).
 template <int L>
 __global__ __launch_bounds__(kThreads) void qknorm_rope_generic_kernel(QkNormRopeParams p) {
     const int tid = threadIdx.x;
@@ -300,6 +303,13 @@ __global__ __launch_bounds__(kThreads) void qknorm_rope_generic_kernel(QkNormRop
 #pragma unroll
     for (int e = 0; e < 4; ++e) packed[e] = (int)pack_bf16x2(out[2 * e], out[2 * e + 1]);
     *(i32x4*)(ref.y + col0) = packed;
+    if (p.xc != nullptr && ref.which == 0) {
+        const uint16_t* xc = (const uint16_t*)p.xc + (int64_t)ref.b * p.xc_sb + (int64_t)ref.s * p.xc_ss +
+                             (int64_t)ref.h * p.xc_sh + col0;
+        uint16_t* yc = (uint16_t*)p.yc + (int64_t)ref.b * p.yc_sb + (int64_t)ref.s * p.yc_ss +
+                       head_ofs(p, (int)ref.h, p.yc_sh, p.yc_sg) + col0;
+        *(i32x4*)yc = *(const i32x4*)xc;
+    }
 }
 
 template <int L>

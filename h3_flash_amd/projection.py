@@ -17,13 +17,13 @@ The fused epilogue keeps the reference's rounding order: the projection is
 rounded to bf16 (as the module's linear outputs it), then normalised and
 rotated in fp32 and rounded once more. (Normalising the fp32 accumulator
 instead, with a single rounding, moved the LSE of the attention that follows
-by up to about 2e-3 against that order at 40 heads.) It reads the RoPE tables in their rotate-half form (columns
-``c`` and ``c + R/2`` equal, which is how every RoPE table of the H3 path is
-built: ``cos(cat(theta, theta))``); tables of another form, a rotary width
-that is not a multiple of 32, non-bf16 weights or a head size other than 128
-make :func:`qkv_projection` return ``None`` so the caller keeps the unfused
-path; so does a call without RoPE, where the reference applies the module's
-own norms.
+by up to about 2e-3 against that order at 40 heads.) Any even rotary width
+up to 128 is taken; RoPE tables in the rotate-half form (columns ``c`` and
+``c + R/2`` equal, ``cos(cat(theta, theta))``) with R a multiple of 32 are
+read at their first half only, others at every rotated column. Non-bf16
+weights, a head size other than 128 or a call without RoPE (where the
+reference applies the module's own norms) make :func:`qkv_projection`
+return ``None``, with the reason, so the caller keeps the unfused path.
 """
 
 from __future__ import annotations
@@ -63,12 +63,16 @@ def proj_gemm(
     cos: torch.Tensor | None = None,
     sin: torch.Tensor | None = None,
     seqlen: int | None = None,
+    rotate_half: bool = True,
 ) -> None:
     """Launch ``h3a_proj_gemm`` on the current stream.
 
     ``x``: (m, k) bf16; each section's ``weight`` (n, k) bf16, ``y`` (m, n)
-    bf16. ``cos``/``sin``: fp32 (seqlen, R) rotate-half tables for the norm
-    sections (token row ``i`` of ``x`` uses table row ``i % seqlen``).
+    bf16. ``cos``/``sin``: fp32 (seqlen, R) tables for the norm sections, R
+    even (token row ``i`` of ``x`` uses table row ``i % seqlen``);
+    ``rotate_half``: the caller's word that columns ``c`` and ``c + R/2``
+    are equal, which lets the epilogue read the first half only (R a
+    multiple of 32); ``False`` reads every rotated column.
     Raises ``ValueError`` for an argument the library rejects and
     ``RuntimeError`` for an unsupported one or a failed launch.
     """
@@ -98,7 +102,7 @@ def proj_gemm(
         args.table_stride = cos.stride(0)
         args.rotary_dim = cos.shape[-1]
         args.seqlen = seqlen if seqlen is not None else cos.shape[0]
-        args.rotate_half_tables = 1
+        args.rotate_half_tables = 1 if rotate_half else 0
     lib = _ext.load_library()
     stream = torch.cuda.current_stream(x.device).cuda_stream
     rc = lib.h3a_proj_gemm(ctypes.byref(args), ctypes.c_void_p(stream))
@@ -147,32 +151,47 @@ def _linear_parts(linear: Any) -> tuple[torch.Tensor, torch.Tensor | None] | Non
 
 
 def qkv_projection(
-    attn: Any, hidden_states: torch.Tensor, rotary_emb: tuple[torch.Tensor, torch.Tensor] | None
+    attn: Any,
+    hidden_states: torch.Tensor,
+    rotary_emb: tuple[torch.Tensor, torch.Tensor] | None,
+    why: list[str] | None = None,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None:
     """q, k, v as (B, S, H, 128) bf16 views of one (B, S, 3*H*128) buffer, q
     and k normalised and rotated in the GEMM epilogue; ``None`` when the
     module or inputs are outside what the fused launch takes (then nothing
-    was launched)."""
+    was launched, and the reason is appended to ``why`` when given).
+
+    Every even rotary width up to 128 is taken (the reference's prologue
+    takes any, src/h3_flash/runtime/kernels/fusions.py:268-275; tables built
+    as _official_rope builds them have R = 6 * len(inv_freq), e.g. 126,
+    src/h3_flash/runtime/parallel/rank_local_io.py:74-80). Tables in the
+    rotate-half form with R a multiple of 32 are read at their first half;
+    others at every rotated column."""
+
+    def no(reason: str):
+        if why is not None:
+            why.append(reason)
+        return None
 
     x = hidden_states
     if x.dim() != 3 or x.dtype != torch.bfloat16 or x.device.type != "cuda":
-        return None
+        return no("hidden_states is not a 3-d bf16 GPU tensor")
     H = getattr(attn, "heads", None)
     if not isinstance(H, int):
-        return None
+        return no("the module has no integer heads")
     B, S, hidden = x.shape
     if hidden % 128 or not x.is_contiguous() or x.data_ptr() % 16 or B * S == 0:
-        return None
+        return no("hidden_states is empty, not contiguous, not 16-byte aligned or its width not a multiple of 128")
     nq, nk = getattr(attn, "norm_q", None), getattr(attn, "norm_k", None)
     wq_n, wk_n = getattr(nq, "weight", None), getattr(nk, "weight", None)
     if not (isinstance(wq_n, torch.Tensor) and isinstance(wk_n, torch.Tensor)):
-        return None
+        return no("norm_q / norm_k carry no weight")
     if wq_n.shape != (HEAD_DIM,) or wk_n.shape != (HEAD_DIM,) or wq_n.dtype != torch.bfloat16 or wk_n.dtype != torch.bfloat16:
-        return None
+        return no("norm weights are not bf16 of head_dim 128")
     if attn.fused_projections:
         parts = _linear_parts(attn.to_qkv)
         if parts is None:
-            return None
+            return no("to_qkv is not a bf16 linear with 16-byte aligned rows")
         w, b = parts
         n = w.shape[0] // 3
         weights = (w[:n], w[n : 2 * n], w[2 * n :])
@@ -180,23 +199,24 @@ def qkv_projection(
     else:
         ps = [_linear_parts(m) for m in (attn.to_q, attn.to_k, attn.to_v)]
         if any(q is None for q in ps):
-            return None
+            return no("to_q / to_k / to_v are not bf16 linears with 16-byte aligned rows")
         weights = tuple(q[0] for q in ps)
         biases = tuple(q[1] for q in ps)
         n = weights[0].shape[0]
         if any(w.shape[0] != n for w in weights):
-            return None
+            return no("to_q / to_k / to_v differ in width")
     if n != H * HEAD_DIM or hidden % K_MULTIPLE or any(w.shape[1] != hidden for w in weights):
-        return None
+        return no("projection widths do not match heads * 128, or hidden is not a multiple of 128")
     if rotary_emb is None:
-        return None  # without RoPE the module's own norms apply (transformer.py:155-158)
+        # without RoPE the module's own norms apply (transformer.py:155-158)
+        return no("no rotary_emb: the module's own norms apply")
     cos, sin = rotary_emb
-    if cos.dim() != 2 or cos.shape[0] != S or cos.shape[-1] % 32 or cos.shape[-1] > HEAD_DIM or sin.shape != cos.shape:
-        return None
+    R = cos.shape[-1] if cos.dim() == 2 else -1
+    if cos.dim() != 2 or cos.shape[0] != S or R % 2 or R > HEAD_DIM or sin.shape != cos.shape:
+        return no(f"rotary tables of shape {tuple(cos.shape)} / {tuple(sin.shape)} for {S} tokens (even R <= 128 taken)")
     # Checked on the caller's own table objects (the conversions below may
     # make fresh temporaries); a dtype or layout change keeps the form.
-    if not rotate_half_tables(cos, sin):
-        return None
+    half_form = rotate_half_tables(cos, sin) if R % 32 == 0 and R > 0 else False
     cos = cos.to(device=x.device, dtype=torch.float32)
     sin = sin.to(device=x.device, dtype=torch.float32)
     if not (cos.is_contiguous() and sin.is_contiguous()):
@@ -209,7 +229,7 @@ def qkv_projection(
         Section(weights[1], y[:, n : 2 * n], biases[1], wk_n, nk.eps),
         Section(weights[2], y[:, 2 * n :], biases[2]),
     ]
-    proj_gemm(x.view(B * S, hidden), sections, cos, sin, S)
+    proj_gemm(x.view(B * S, hidden), sections, cos, sin, S, rotate_half=half_form)
     q, k, v = out.chunk(3, dim=-1)
     return q.unflatten(-1, (H, HEAD_DIM)), k.unflatten(-1, (H, HEAD_DIM)), v.unflatten(-1, (H, HEAD_DIM))
 

@@ -31,7 +31,7 @@ import torch
 
 from . import _ext
 from .attention import flash_attn_func
-from .prologue import _check_rotary, _tables, _weight, fused_qk_norm_rope
+from .prologue import _check_rotary, _tables, _weight
 
 __all__ = [
     "can_pack_qkv",
@@ -159,8 +159,9 @@ def qknorm_rope_pack_qkv(
 
     q, k, v: (rows, heads, head_dim) bf16; cos/sin: fp32 (rows, R). The
     result is bit-identical to ``pack_qkv_destination_major(fused_qknorm_rope(q),
-    fused_qknorm_rope(k), v, world)``. Rotary widths that are not a multiple
-    of 16 run as those two HIP launches.
+    fused_qknorm_rope(k), v, world)``, for every even rotary width R <= D
+    (the reference's prologue takes any, fusions.py:268-275; tables built as
+    _official_rope builds them have R = 6 * len(inv_freq), e.g. 126).
     """
 
     if not (q.shape == k.shape == v.shape):
@@ -178,12 +179,6 @@ def qknorm_rope_pack_qkv(
     if wq.dtype != wk.dtype:
         wq, wk = wq.float(), wk.float()
     cos, sin = _tables(cos, sin, rows, q.device)
-    aligned = cos.data_ptr() % 16 == 0 and sin.data_ptr() % 16 == 0 and cos.stride(0) % 4 == 0
-    if R % 16 != 0 or not aligned:
-        qn, kn = fused_qk_norm_rope(
-            q.unsqueeze(0), k.unsqueeze(0), wq, wk, cos, sin, eps_q, eps_k
-        )
-        return pack_qkv_destination_major(qn.squeeze(0), kn.squeeze(0), v, world)
     out = torch.empty((world, rows, heads // world, 3 * head_dim), dtype=q.dtype, device=q.device)
     if out.numel() == 0:
         return out

@@ -276,10 +276,11 @@ H3A_API int h3a_merge_heads(const h3a_merge_heads_args *args, void *stream);
  * ((rows, heads, head_dim) bf16, strides {row, head}) are normalised and
  * rotated exactly as by h3a_qknorm_rope (same arithmetic, same rounding) and
  * written, with v copied verbatim, into the destination-major buffer `out`
- * of h3a_pack_qkv. Batch is 1 (the packed path's only case). Requires a
- * rotary width that is a multiple of 16 (or 0) and 16-byte aligned cos/sin
- * rows; other widths return H3A_EUNSUPPORTED (compose h3a_qknorm_rope and
- * h3a_pack_qkv instead).
+ * of h3a_pack_qkv. Batch is 1 (the packed path's only case). Any even
+ * rotary width up to head_dim, as for h3a_qknorm_rope; cos/sin 4-byte
+ * aligned (a rotary width that is a multiple of 16 with 16-byte aligned
+ * table rows takes the vectorised kernel, others an element-wise one with
+ * the same results).
  */
 typedef struct h3a_qknorm_rope_pack_args {
     int32_t abi_version;
@@ -464,10 +465,14 @@ H3A_API int h3a_attn_merge(const h3a_attn_merge_args *args, void *stream);
  * one launch. head_dim must be 128; k a positive multiple of 128; each n a
  * positive multiple of 128; x, weight and y 16-byte aligned with strides that
  * are multiples of 8 elements; bias and norm_weight (bf16) 8-byte aligned;
- * rotary_dim a multiple of 32 (other widths: a PLAIN projection followed by
- * h3a_qknorm_rope); cos / sin fp32 (seqlen rows of table_stride floats),
- * 16-byte aligned, table_stride a multiple of 4. No workspace; nothing is
- * allocated.
+ * rotary_dim any even width up to 128 (as fused_qknorm_rope takes,
+ * fusions.py:268-275); cos / sin fp32 (seqlen rows of table_stride >=
+ * rotary_dim floats), 4-byte aligned. With rotary_dim a multiple of 32,
+ * rotate_half_tables = 1 and 16-byte aligned table rows (table_stride a
+ * multiple of 4), each lane holds its RoPE partners and only the tables'
+ * first half is read; otherwise the partners come from the token's other
+ * lanes through LDS and the tables are read at every rotated column (same
+ * results). No workspace; nothing is allocated.
  */
 #define H3A_PROJ_PLAIN 0
 #define H3A_PROJ_QKNORM_ROPE 1
@@ -497,12 +502,13 @@ typedef struct h3a_proj_args {
     const float *cos;   /* fp32 (seqlen, table_stride), or NULL when rotary_dim is 0 */
     const float *sin;
     int64_t table_stride;
-    int64_t rotary_dim; /* 0, 32, 64, 96 or 128 */
+    int64_t rotary_dim; /* even, 0 .. 128 */
     int64_t seqlen;     /* table rows; token row m uses row m % seqlen */
-    int32_t rotate_half_tables; /* must be 1 when rotary_dim > 0: the caller guarantees
-                                   cos[:, c] == cos[:, c + R/2] and sin[:, c] == sin[:, c + R/2]
-                                   (the cat(theta, theta) form of rotate-half RoPE tables);
-                                   only the first R/2 columns are read */
+    int32_t rotate_half_tables; /* 1: the caller guarantees cos[:, c] == cos[:, c + R/2] and
+                                   sin[:, c] == sin[:, c + R/2] (the cat(theta, theta) form of
+                                   rotate-half RoPE tables), which lets a rotary_dim that is a
+                                   multiple of 32 read the first R/2 columns only; 0: tables of
+                                   any form, read at every rotated column */
 } h3a_proj_args;
 
 H3A_API int h3a_proj_gemm(const h3a_proj_args *args, void *stream);

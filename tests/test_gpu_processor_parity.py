@@ -13,8 +13,12 @@ A kernel wrapper records what the processor hands the kernel (q, k, v) and
 what the kernel returns (out, LSE). Out and LSE must meet the path's bar
 against the oracle (max abs <= 2e-2, mean abs <= 2e-3, |dLSE| <= 1e-3), for
 the processor as constructed by default (hipBLASLt projections + the HIP
-prologue), for the fused projection GEMM (q/k rounded once, from the fp32
-accumulator), and for both projection layouts (to_qkv and to_q/to_k/to_v).
+prologue), for the fused projection GEMM (its epilogue rounds the
+projection to bf16 before the norm, as the reference does; rounding once,
+from the fp32 accumulator, measured LSE errors of 1.9-2.1e-3 here), for both
+projection layouts (to_qkv and to_q/to_k/to_v), with the 44/42/42 3D tables
+and with tables built as _official_rope builds them (21 shared frequencies,
+R = 126).
 The q/k the processor produced must lie within the bound that rounding the
 projection first sets on the CPU (tests/test_oracle_projection.py: 2^-4 at
 most, 2^-8 on average).
@@ -105,29 +109,47 @@ def reference_order(attn: H3Attention, x: torch.Tensor, cos, sin):
     return q, k, v
 
 
+def official_rope_tables(grid, n_freq: int = 21, base: float = 10000.0):
+    """Tables built as _official_rope builds them (rank_local_io.py:74-80):
+    one inv_freq of n_freq entries for every axis, angles cat(t f, h f, w f)
+    repeated, so R = 6 * n_freq (126 for 21 frequencies)."""
+
+    inv = 1.0 / base ** (torch.arange(0, 2 * n_freq, 2, dtype=torch.float32) / (2 * n_freq))
+    T, Hp, Wp = grid
+    n = torch.arange(T * Hp * Wp)
+    pos = torch.stack((n // (Hp * Wp), (n // Wp) % Hp, n % Wp), dim=-1).float()
+    theta = torch.cat([pos[:, a : a + 1] * inv[None, :] for a in range(3)], dim=-1)
+    theta = torch.cat((theta, theta), dim=-1)
+    return theta.cos(), theta.sin()
+
+
 @pytest.mark.parametrize(
-    "fused_module,fuse_projections",
-    [(True, None), (False, None), (True, True), (False, True)],
-    ids=["to_qkv-default", "to_q_k_v-default", "to_qkv-fused-gemm", "to_q_k_v-fused-gemm"],
+    "fused_module,fuse_projections,tables",
+    [(True, None, "3d"), (False, None, "3d"), (True, True, "3d"), (False, True, "3d"), (True, True, "r126"),
+     (False, None, "r126")],
+    ids=["to_qkv-default", "to_q_k_v-default", "to_qkv-fused-gemm", "to_q_k_v-fused-gemm", "to_qkv-fused-gemm-R126",
+         "to_q_k_v-default-R126"],
 )
-def test_processor_attention_meets_the_path_tolerance(fused_module, fuse_projections):
+def test_processor_attention_meets_the_path_tolerance(fused_module, fuse_projections, tables):
     attn = H3Attention(fused_module, seed=31 + fused_module).to(torch.bfloat16)
     g = torch.Generator().manual_seed(7)
     x = torch.randn((1, S, HIDDEN), generator=g).to(torch.bfloat16)
-    cos, sin = rope_3d_tables(GRID)
+    cos, sin = rope_3d_tables(GRID) if tables == "3d" else official_rope_tables(GRID)
     q_ref, k_ref, v_ref = reference_order(attn, x, cos, sin)
 
     kernel = RecordingKernel()
     kw = {} if fuse_projections is None else {"fuse_projections": fuse_projections}
     processor = DenseMiniMaxH3Processor(kernel=kernel, **kw)
+    processor._audit = {}
     attn = attn.to(DEV)
     with torch.no_grad():
         block = processor(attn, x.to(DEV), (cos.to(DEV), sin.to(DEV)))
     torch.cuda.synchronize()
+    assert processor._audit.get("projection_fallbacks", {}) == {}  # the fused launch ran when asked for
     assert processor.calls == 1 and kernel.record is not None
     assert block.shape == (1, S, HIDDEN) and torch.isfinite(block.float()).all()
     q, k, v, out, lse = (t.cpu() for t in kernel.record)
-    tag = (fused_module, fuse_projections)
+    tag = (fused_module, fuse_projections, tables, cos.shape[-1])
 
     # what reached the kernel: v is the bf16 projection (hipBLASLt, which may
     # round the product before adding the bias, or the GEMM's plain section)

@@ -1,9 +1,12 @@
-"""The projection GEMM (h3a_proj_gemm) on the GPU against the CPU oracle:
-plain sections and sections with the q/k RMSNorm + RoPE epilogue, ragged
-token counts, half-width last tiles, every admitted rotary width, the
-persistent grid with several tiles per workgroup, the 480p rank and 40-head
-projection shapes (sampled rows), hipBLASLt's own linear, and the attention
-processor with fused projections."""
+"""The projection GEMM (h3a_proj_gemm) on the GPU against the CPU oracle in
+the reference's rounding order (the projection rounded to bf16, then the q/k
+RMSNorm + RoPE): plain sections and sections with the norm + RoPE epilogue,
+ragged token counts, half-width last tiles, rotary widths that are multiples
+of 32 (partners in the same lane, the tables' first half read) and any other
+even width or table form (partners from the token's other lanes, every
+rotated column read), more tiles than CUs (one workgroup per tile), the 480p
+rank and 40-head projection shapes (sampled rows), hipBLASLt's own linear,
+and the attention processor with fused projections and its fallback record."""
 
 from __future__ import annotations
 
@@ -12,7 +15,7 @@ import math
 import pytest
 import torch
 
-from h3_flash_amd import DenseMiniMaxH3Processor
+from h3_flash_amd import DenseMiniMaxH3Processor, install_dense_hip
 from h3_flash_amd.projection import Section, out_projection, proj_gemm, qkv_projection, rotate_half_tables
 from h3_flash_amd.rope import rope_3d_tables
 from oracle.metrics import error_metrics
@@ -69,7 +72,7 @@ def make(M, K, heads, R, bias, seed=0):
     return x, w, b, nwq, nwk
 
 
-def run_qkv(x, w, b, nwq, nwk, cos, sin, seqlen, eps=1e-6):
+def run_qkv(x, w, b, nwq, nwk, cos, sin, seqlen, eps=1e-6, rotate_half=True):
     n = w.shape[0] // 3
     xd, wd = x.to(DEV), w.to(DEV)
     bd = b.to(DEV) if b is not None else None
@@ -80,7 +83,7 @@ def run_qkv(x, w, b, nwq, nwk, cos, sin, seqlen, eps=1e-6):
         Section(wd[2 * n :], y[:, 2 * n :], None if bd is None else bd[2 * n :]),
     ]
     c, s = (None, None) if cos is None else (cos.to(DEV), sin.to(DEV))
-    proj_gemm(xd, secs, c, s, seqlen)
+    proj_gemm(xd, secs, c, s, seqlen, rotate_half=rotate_half)
     torch.cuda.synchronize()
     return y.cpu()
 
@@ -125,9 +128,35 @@ def test_3d_rope_tables_of_the_480p_grid():
     check_qkv(x, w, b, nwq, nwk, cos, sin, S, y)
 
 
+@pytest.mark.parametrize(
+    "R, form",
+    [(126, "rotate-half"), (42, "rotate-half"), (2, "rotate-half"), (96, "any"), (128, "rotate-half, read whole")],
+)
+def test_any_even_rotary_width(R, form):
+    # widths that are not a multiple of 32 (R = 6 * 21 from a 21-frequency
+    # 3D table, as _official_rope builds it: rank_local_io.py:74-80) and
+    # tables in another form: partners from the token's other lanes, tables
+    # read at every rotated column
+    M, K, heads = 520, 256, 2
+    x, w, b, nwq, nwk = make(M, K, heads, R, True, seed=R)
+    if form == "any":
+        g = torch.Generator().manual_seed(R)
+        ang = torch.rand((M, R), generator=g) * 6.0
+        cos, sin = ang.cos(), ang.sin()
+        assert not rotate_half_tables(cos, sin)
+    else:
+        cos, sin = tables(M, R, seed=3)
+    y = run_qkv(x, w, b, nwq, nwk, cos, sin, M, rotate_half=form == "rotate-half")
+    check_qkv(x, w, b, nwq, nwk, cos, sin, M, y)
+    # table rows wrapping per sequence, with sampled rows
+    y = run_qkv(x, w, b, nwq, nwk, cos[:130], sin[:130], 130, rotate_half=form == "rotate-half")
+    check_qkv(x, w, b, nwq, nwk, cos[:130], sin[:130], 130, y)
+
+
 def test_more_tiles_than_cus():
-    # 17 token tiles x 60 feature tiles: four rounds of workgroups over the
-    # XCDs' tile ranges, the last token tile ragged
+    # 17 token tiles x 60 feature tiles: 1,020 workgroups (one per tile),
+    # about four per CU, each XCD a contiguous range; the last token tile
+    # ragged
     x, w, b, nwq, nwk = make(4096 + 96, 256, 40, 128, True, seed=7)
     cos, sin = tables(4192, 128, seed=1)
     y = run_qkv(x, w, b, nwq, nwk, cos, sin, 4192)
@@ -245,16 +274,48 @@ def test_processor_with_fused_projections(fused):
         assert m["finite"] and m["relative_l2"] < 1e-2 and m["cosine"] > 0.9999, (key, m)
 
 
-def test_other_tables_keep_the_separate_steps():
+def test_tables_of_any_form_take_the_fused_launch():
+    # tables that are not in the rotate-half form are read at every rotated
+    # column: the fused launch runs and matches the separate steps
     attn = H3Attention(1, False).to(torch.bfloat16).to(DEV)
     x = torch.randn((1, 64, 128), device=DEV).to(torch.bfloat16)
     cos, sin = torch.rand((64, 128), device=DEV), torch.rand((64, 128), device=DEV)  # not rotate-half
     assert not rotate_half_tables(cos, sin)
-    assert qkv_projection(attn, x, (cos, sin)) is None
-    assert qkv_projection(attn, x, None) is None  # the module's own norms apply without RoPE
-    processor = DenseMiniMaxH3Processor(fuse_projections=True)
+    why = []
+    fused = qkv_projection(attn, x, (cos, sin), why)
+    assert fused is not None and why == []
+    processor = DenseMiniMaxH3Processor(fuse_projections=False)
     attn.set_processor(processor)
     with torch.no_grad():
-        out = attn(x, rotary_emb=(cos, sin))
+        q, k, v = processor._projections(attn, x, (cos, sin))
     torch.cuda.synchronize()
-    assert processor.calls == 1 and torch.isfinite(out.float()).all()
+    for got, want in zip(fused, (q, k, v)):
+        d = (got.float() - want.float()).abs()
+        assert d.max() <= 2.0**-4 and d.mean() <= 2.0**-10, float(d.max())
+
+
+def test_fallbacks_are_recorded_in_the_install_audit():
+    class Transformer(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.blocks = torch.nn.ModuleList([H3Attention(1, False) for _ in range(2)])
+
+    t = Transformer().to(torch.bfloat16).to(DEV)
+    record = install_dense_hip(t, H3Attention, fuse_projections=True)
+    assert record["fuse_projections"] is True and record["projection_fallbacks"] == {}
+    x = torch.randn((1, 64, 128), device=DEV).to(torch.bfloat16)
+    cos, sin = (z.to(DEV) for z in rope_3d_tables((1, 8, 8)))
+    with torch.no_grad():
+        for blk in t.blocks:
+            blk(x, rotary_emb=(cos, sin))  # fused: nothing recorded
+        assert record["projection_fallbacks"] == {}
+        for blk in t.blocks:
+            blk(x)  # no RoPE: the module's own norms, recorded per call
+        odd = torch.rand((64, 7), device=DEV)
+        with pytest.raises(ValueError):
+            t.blocks[0](x, rotary_emb=(odd, odd))  # an odd width: recorded, then the prologue refuses it
+    torch.cuda.synchronize()
+    fb = record["projection_fallbacks"]
+    assert fb["no rotary_emb: the module's own norms apply"] == 2
+    assert sum(v for k, v in fb.items() if k.startswith("rotary tables of shape (64, 7)")) == 1
+    assert qkv_projection(t.blocks[0], x, None) is None  # the module's own norms apply without RoPE

@@ -137,7 +137,7 @@ def test_merge_strided_input():
     assert np.array_equal(_bits(merge_heads(y)), merge_heads_permute(_bits(y)))
 
 
-@pytest.mark.parametrize("R", [128, 96, 0, 42])
+@pytest.mark.parametrize("R", [128, 96, 0, 42, 126, 2])
 @pytest.mark.parametrize("wdtype", [torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("heads, world", [(40, 8), (6, 3), (7, 7)])  # whole and partial head chunks
 def test_fused_prologue_pack_equals_unfused(R, wdtype, heads, world):
