@@ -49,6 +49,7 @@ def parse_args(argv=None):
     p.add_argument("--no-relayout", action="store_true", help="skip the relayout, row-fusion and context-parallel merge rates")
     p.add_argument("--no-block", action="store_true", help="skip the whole-attention-block timing")
     p.add_argument("--no-sdpa", action="store_true", help="skip torch's GPU SDPA and the numerical comparison with it")
+    p.add_argument("--no-wide", action="store_true", help="skip the long to_qkv-view attention (the kernel's wide form)")
     p.add_argument(
         "--copy-calibration",
         type=int,
@@ -140,6 +141,49 @@ def _time_ms(torch, fn, reps: int = 20) -> float:
     b.record(stream)
     torch.cuda.synchronize()
     return a.elapsed_time(b) / reps
+
+
+def wide_view_rates(torch, heads: int = 40, seqlen: int = 72003, head_dim: int = 128, reps: int = 3) -> dict:
+    """Attention on ``to_qkv(...).chunk(3)`` views of one (1, S, 3*H*D)
+    buffer, the form the reference's processor hands the kernel
+    (dense_fa4.py:123-131,145), at a length where a view's rows span 2^31
+    bytes or more (40 heads: beyond about 69,000 tokens), so the kernel runs
+    its wide form (buffer resources rebased per query tile and per window of
+    keys); next to the same q, k, v as contiguous tensors (the narrow form),
+    on the same inputs. Outputs must be bit-identical."""
+
+    from h3_flash_amd import flash_attn_func
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(41)
+    qkv = torch.randn((1, seqlen, 3 * heads * head_dim), device=dev, generator=g).to(torch.bfloat16)
+    q, k, v = (t.unflatten(-1, (heads, head_dim)) for t in qkv.chunk(3, dim=-1))
+    span = (seqlen - 1) * q.stride(1) * 2 + head_dim * 2
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    flop = 4.0 * seqlen * seqlen * head_dim * heads
+    with torch.no_grad():
+        o_view = flash_attn_func(q, k, v)[0]
+        o_copy = flash_attn_func(qc, kc, vc)[0]
+        view_ms = _time_ms(torch, lambda: flash_attn_func(q, k, v), reps=reps)
+        copy_ms = _time_ms(torch, lambda: flash_attn_func(qc, kc, vc), reps=reps)
+        view_ms = min(view_ms, _time_ms(torch, lambda: flash_attn_func(q, k, v), reps=reps))
+        copy_ms = min(copy_ms, _time_ms(torch, lambda: flash_attn_func(qc, kc, vc), reps=reps))
+    torch.cuda.synchronize()
+    out = {
+        "workload": f"to_qkv views: B=1 H={heads} S={seqlen} D={head_dim}, row stride {q.stride(1)} elements "
+        f"(a view spans {span / 2**30:.2f} GiB), against contiguous copies",
+        "view_span_bytes": span,
+        "wide_form": span >= 2**31,
+        "views_ms": view_ms,
+        "contiguous_ms": copy_ms,
+        "views_TFLOP_s": flop / (view_ms * 1e-3) / 1e12,
+        "contiguous_TFLOP_s": flop / (copy_ms * 1e-3) / 1e12,
+        "views_vs_contiguous": copy_ms / view_ms,
+        "bit_identical": bool(torch.equal(o_view, o_copy)),
+    }
+    del qkv, q, k, v, qc, kc, vc, o_view, o_copy
+    torch.cuda.empty_cache()
+    return out
 
 
 def relayout_rates(torch, world: int = 8, heads: int = 40, seqlen: int = 49920, head_dim: int = 128) -> dict:
@@ -716,6 +760,7 @@ def main(argv=None) -> int:
     # the whole 480p/5s sequence on one GPU (no Ulysses split), 40 heads
     result["fusions_full_sequence"] = None if args.no_relayout else fusion_rates(torch, rows=49920, hidden=5120)
     result["cp_merge"] = None if args.no_relayout else merge_rates(torch)
+    result["wide_views"] = None if args.no_wide else wide_view_rates(torch)
     result["block"] = None if args.no_block else block_rates(torch)
     result["projections"] = None if args.no_block else projection_rates(torch)
     if not args.no_cpu_baseline:

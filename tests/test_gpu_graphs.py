@@ -3,7 +3,9 @@ serving loop would replay it: the prologue, the attention with its
 split-tail workspace and merge kernel, the attention's dynamic tail (its
 counter is reset by a kernel recorded in the graph), a packed varlen launch
 whose work list is planned on the device (the segmentation changes between
-replays: the recorded planning kernel reads the new offsets), and a row
+replays: the recorded planning kernel reads the new offsets), a packed
+launch of short segments on the persistent kernel (its tile counter reset by
+a recorded kernel; the segmentation changes between replays), and a row
 fusion. Each replay runs on new inputs written into the captured buffers by
 eager work, and must equal the eager launches on the same inputs bit for bit
 (same kernels, same launch shapes, deterministic)."""
@@ -82,3 +84,56 @@ def test_prologue_attention_and_fusion_replay_in_a_graph():
     o, l, full, full_lse = captured[:4]
     assert (o.float() - full.float()).abs().max().item() <= 2e-2
     assert (l - full_lse).abs().max().item() <= 1e-3
+
+
+@pytest.mark.parametrize("heads", [5, 40])
+def test_persistent_short_segment_launch_replays_in_a_graph(heads):
+    # a packed launch whose longest segment is under 4,096 rows runs one
+    # workgroup per CU that claims tiles from a counter (reset by a kernel
+    # recorded in the graph); the segmentation changes between replays, the
+    # number of segments (and max_seqlen_q) staying what was captured
+    rows, D, max_q = 9000, 128, 3000
+    q, k, v = (torch.empty((1, rows, heads, D), dtype=torch.bfloat16, device=DEV) for _ in range(3))
+    segmentations = (
+        [0, 1024, 2048, 5000, 8000, 9000],
+        [0, 3000, 6000, 9000, 9000, 9000],
+        [0, 1, 2000, 4500, 7000, 9000],
+        [0, 0, 2999, 5998, 8997, 9000],
+        [0, 700, 1400, 4000, 6500, 9000],
+    )
+    cu = torch.tensor(segmentations[0], dtype=torch.int32, device=DEV)
+
+    def step():
+        return flash_attn_func(q, k, v, cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max_q)
+
+    _fill([q, k, v], heads)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = step()
+    torch.cuda.synchronize()
+
+    for replay in range(4):
+        _fill([q, k, v], 200 + replay)
+        cu.copy_(torch.tensor(segmentations[replay + 1], dtype=torch.int32))
+        eager = [t.clone() for t in step()]
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, got, want in zip(("out", "lse"), captured, eager):
+            assert torch.equal(got, want), f"replay {replay}: {name} differs from the eager launch"
+        # and the segments really are independent: the last segment's rows
+        # equal a standalone launch over them (whole tiles, as the packed
+        # launch runs them)
+        a, e = segmentations[replay + 1][-2], segmentations[replay + 1][-1]
+        if e > a:
+            alone = flash_attn_func(
+                q[:, a:e].contiguous(), k[:, a:e].contiguous(), v[:, a:e].contiguous(), split_tail=False
+            )
+            torch.cuda.synchronize()
+            assert torch.equal(captured[0][:, a:e], alone[0]), replay
