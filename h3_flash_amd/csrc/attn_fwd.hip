@@ -39,7 +39,7 @@
 #include "common.h"
 #include "kernels.h"
 
-// Workspace of h3a_attn_fwd_noalloc: the fp32 partial results of the tail's
+// Workspace of h3a_attn_fwd_noalloc: the partial results (bf16 O, fp32 LSE) of the tail's
 // key-range pieces and the tail's counter, for callers that cannot allocate.
 // Every GPU the library runs on holds its own copy until the process ends.
 // Host code never passes `scratch` itself (on the host it names a shadow
@@ -788,16 +788,19 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
     const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
     const float lse = l_run > 0.f ? (mc + __log2f(l_run)) * 0.69314718055994531f : -INFINITY;
     if (slot >= 0) {
-        // Partial result of a key-range piece: normalised O and LSE in fp32.
+        // Partial result of a key-range piece: normalised O in bf16 (as the
+        // output itself is rounded) and the LSE in fp32.
         const int row = wave * 32 + l32;
-        float* wo = p.ws_o + ((int64_t)slot * kBM + row) * kD;
+        uint16_t* wo = p.ws_o + ((int64_t)slot * kBM + row) * kD;
 #pragma unroll
         for (int db = 0; db < 4; ++db)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int d = db * 32 + i * 8 + hi * 4;
-                *(f32x4*)(wo + d) = f32x4{oacc[db][i * 4 + 0] * inv, oacc[db][i * 4 + 1] * inv,
-                                          oacc[db][i * 4 + 2] * inv, oacc[db][i * 4 + 3] * inv};
+                i32x2 w;
+                w.x = (int)pack_bf16x2(oacc[db][i * 4 + 0] * inv, oacc[db][i * 4 + 1] * inv);
+                w.y = (int)pack_bf16x2(oacc[db][i * 4 + 2] * inv, oacc[db][i * 4 + 3] * inv);
+                *(i32x2*)(wo + d) = w;
             }
         if (hi == 0) p.ws_lse[(int64_t)slot * kBM + row] = lse;
         return false;
@@ -1209,15 +1212,15 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
     const int mq = qt * kBM + row;
     if (mq >= sq) return;
     float lq[kMaxP];
-    f32x4 part[kMaxP][4];
+    i32x4 part[kMaxP][2];  // 16 bf16 head dims of the row per piece
 #pragma unroll
     for (int c = 0; c < kMaxP; ++c) {
         if (c >= n) break;
         const int64_t pc = slot0 + c * slot_step;
         lq[c] = p.ws_lse[pc * kBM + row];
-        const f32x4* src = (const f32x4*)(p.ws_o + (pc * kBM + row) * kD + d0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) part[c][i] = src[i];
+        const i32x4* src = (const i32x4*)(p.ws_o + (pc * kBM + row) * kD + d0);
+        part[c][0] = src[0];
+        part[c][1] = src[1];
     }
     float lse_max = -INFINITY;
 #pragma unroll
@@ -1235,7 +1238,12 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
         const float w = lq[c] == -INFINITY ? 0.f : __expf(lq[c] - lse_max);
         wsum += w;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] += w * part[c][i];
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t lo = (uint32_t)part[c][i >> 1][2 * (i & 1)], up = (uint32_t)part[c][i >> 1][2 * (i & 1) + 1];
+            const f32x4 x{__uint_as_float(lo << 16), __uint_as_float(lo & 0xffff0000u), __uint_as_float(up << 16),
+                          __uint_as_float(up & 0xffff0000u)};
+            acc[i] += w * x;
+        }
     }
     const float inv = wsum > 0.f ? 1.0f / wsum : 0.f;
     char* ob = (char*)p.o + 2 * (b * p.o_sb + h * p.o_sh + d0) + (int64_t)(q0 + mq) * p.o_rs;
@@ -1259,7 +1267,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
 int attn_fwd_block_m() { return kBM; }
 int attn_fwd_persist_max_rows() { return kPersistMaxQTiles * kBM; }
 int attn_fwd_tail_pieces() { return kQueuePieces; }
-int64_t attn_fwd_piece_bytes() { return (int64_t)kBM * (kD + 1) * (int64_t)sizeof(float); }
+int64_t attn_fwd_piece_bytes() { return (int64_t)kBM * (kD * 2 + 4); }
 int attn_fwd_block_n() { return kBN; }
 int attn_fwd_window_rows() { return kWindowRows > kBM ? kWindowRows : kBM; }
 int attn_fwd_row_margin() { return kBM + kBN * (2 * kStages + 2); }
@@ -1267,7 +1275,7 @@ int attn_fwd_row_margin() { return kBM + kBN * (2 * kStages + 2); }
 SplitPlan plan_attn_split(int64_t tiles, int64_t key_tiles, int cus, int64_t max_workspace) {
     SplitPlan plan{(int32_t)tiles, 0, 0, 0, 0, 0};
     if (cus < 8 || cus % 8 != 0 || tiles <= 0) return plan;
-    const int64_t piece_bytes = (int64_t)kBM * (kD + 1) * (int64_t)sizeof(float);
+    const int64_t piece_bytes = attn_fwd_piece_bytes();  // bf16 partial O and fp32 LSE of a piece's rows
     if (tiles > cus) {
         // Dynamic tail: the whole rounds but the last run as they are; the
         // last round's tiles become kQueuePieces key-range pieces each, taken

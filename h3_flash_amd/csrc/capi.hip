@@ -226,8 +226,8 @@ void apply_plan(h3a::AttnParams& p, const h3a::SplitPlan& plan, void* workspace)
     p.n_full = plan.n_full;
     p.split_n = plan.split_n;
     p.split_tiles = plan.split_tiles;
-    p.ws_o = (float*)workspace;
-    p.ws_lse = p.ws_o + (int64_t)plan.split_n * plan.split_tiles * h3a::attn_fwd_block_m() * 128;
+    p.ws_o = (uint16_t*)workspace;
+    p.ws_lse = (float*)(p.ws_o + (int64_t)plan.split_n * plan.split_tiles * h3a::attn_fwd_block_m() * 128);
     if (plan.queue_blocks > 0) {
         p.queue = (int*)((char*)workspace + plan.queue_offset);
         p.queue_blocks = plan.queue_blocks;
@@ -312,8 +312,8 @@ int h3a_attn_fwd(const h3a_attn_args* a, void* stream) {
         }
         if (w.ub_tiles > 0) {
             const int64_t pieces = (int64_t)h3a::attn_fwd_tail_pieces() * w.cus;
-            p.ws_o = (float*)a->workspace;
-            p.ws_lse = p.ws_o + pieces * h3a::attn_fwd_block_m() * 128;
+            p.ws_o = (uint16_t*)a->workspace;
+            p.ws_lse = (float*)(p.ws_o + pieces * h3a::attn_fwd_block_m() * 128);
             int32_t* words = (int32_t*)((char*)a->workspace + w.plan_offset);
             p.vplan = p.vplan_w = words;
             p.vlist = p.vlist_w = words + h3a::kPlanWords;

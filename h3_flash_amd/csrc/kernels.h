@@ -31,13 +31,13 @@ struct AttnParams {
     const int32_t* cu_k;
     // Key-range split of the last tiles (dense only; split_n == 0: none).
     // Tiles [0, n_full) run whole; tiles [n_full, n_full + split_tiles) run as
-    // split_n pieces each, which write normalised fp32 partial O and LSE to
-    // ws_o / ws_lse for attn_merge to combine.
+    // split_n pieces each, which write normalised bf16 partial O and fp32
+    // LSE to ws_o / ws_lse for attn_merge to combine.
     int32_t n_full;
     int32_t split_n;
     int32_t split_tiles;
-    float* ws_o;    // [split_n * split_tiles][kBM][128]
-    float* ws_lse;  // [split_n * split_tiles][kBM]
+    uint16_t* ws_o;  // bf16 [split_n * split_tiles][kBM][128], normalised
+    float* ws_lse;   // [split_n * split_tiles][kBM]
     // Dynamic tail (queue != NULL): workgroups [0, n_full) run whole tiles;
     // the queue_blocks workgroups after them take piece indices
     // [0, split_n * split_tiles) from *queue, which the launch zeroes, until

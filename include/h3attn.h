@@ -105,9 +105,9 @@ extern "C" {
  *     workgroups take from a counter in the workspace as CUs free up; with
  *     fewer tiles, when they would keep less than 70% of the CUs busy (B=1
  *     H=4 S=4096: 64 tiles on 256 CUs), they run as statically assigned
- *     pieces. Either way the fp32 partial results are merged by a second
- *     kernel on the same stream (the counter is zeroed by a small kernel
- *     first);
+ *     pieces. Either way the partial results (normalised bf16 O, fp32 LSE)
+ *     are merged by a second kernel on the same stream (the counter is
+ *     zeroed by a small kernel first);
  *   - a d-major copy of V (per batch and head, 128 rows of keys padded with
  *     zeros to a multiple of 64), written by a transpose kernel at the start
  *     of the call, from which the attention kernel reads each PV fragment
@@ -170,7 +170,7 @@ H3A_API int64_t h3a_attn_fwd_workspace_size(const h3a_attn_args *args);
  *
  * Same arguments, semantics and results (up to the rounding of the key-range
  * pieces) as h3a_attn_fwd; `workspace` / `workspace_bytes` are ignored. The
- * split tail's fp32 partial results and counter live in a file-scope device
+ * split tail's partial results (bf16 O, fp32 LSE) and counter live in a file-scope device
  * array of H3A_NOALLOC_SCRATCH_BYTES (64 MiB) that every GPU the library
  * runs on holds until the process ends; its address is looked up once per
  * device. The split plan is fitted to that array (fewer key-range pieces,

@@ -362,7 +362,7 @@ def test_workspace_plan_on_this_device():
         a.softmax_scale = 0.088
         return lib.h3a_attn_fwd_workspace_size(ctypes.byref(a))
 
-    per_piece = 256 * 129 * 4  # a multiple of 256
+    per_piece = 256 * (128 * 2 + 4)  # bf16 O and an fp32 LSE per row; a multiple of 256
 
     def vt(B, S, H):  # d-major V: 128 rows of keys per (batch, head), padded to 64 keys,
         # for sequences of 16,384 keys or more (shorter ones read V as given)
