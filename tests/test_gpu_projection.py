@@ -130,7 +130,8 @@ def test_3d_rope_tables_of_the_480p_grid():
 
 @pytest.mark.parametrize(
     "R, form",
-    [(126, "rotate-half"), (42, "rotate-half"), (2, "rotate-half"), (96, "any"), (128, "rotate-half, read whole")],
+    [(126, "rotate-half"), (42, "rotate-half"), (2, "rotate-half"), (34, "rotate-half"), (96, "any"),
+     (128, "rotate-half, read whole"), (64, "rotate-half, padded rows")],
 )
 def test_any_even_rotary_width(R, form):
     # widths that are not a multiple of 32 (R = 6 * 21 from a 21-frequency
@@ -146,6 +147,26 @@ def test_any_even_rotary_width(R, form):
         assert not rotate_half_tables(cos, sin)
     else:
         cos, sin = tables(M, R, seed=3)
+    if form == "rotate-half, padded rows":
+        # rows of 66 floats (264 bytes: not 16-byte rows) holding 64 columns,
+        # read in place: the epilogue reads every rotated column
+        n = w.shape[0] // 3
+        y = torch.empty((M, 3 * n), dtype=torch.bfloat16, device=DEV)
+        wd = w.to(DEV)
+        bd = b.to(DEV)
+        secs = [
+            Section(wd[:n], y[:, :n], bd[:n], nwq.to(DEV), 1e-6),
+            Section(wd[n : 2 * n], y[:, n : 2 * n], bd[n : 2 * n], nwk.to(DEV), 1e-6),
+            Section(wd[2 * n :], y[:, 2 * n :], bd[2 * n :]),
+        ]
+        full_c = torch.zeros((M, 66), device=DEV)
+        full_s = torch.zeros((M, 66), device=DEV)
+        full_c[:, :R], full_s[:, :R] = cos.to(DEV), sin.to(DEV)
+        assert full_c[:, :R].stride(0) == 66
+        proj_gemm(x.to(DEV), secs, full_c[:, :R], full_s[:, :R], M, rotate_half=True)
+        torch.cuda.synchronize()
+        check_qkv(x, w, b, nwq, nwk, cos, sin, M, y.cpu())
+        return
     y = run_qkv(x, w, b, nwq, nwk, cos, sin, M, rotate_half=form == "rotate-half")
     check_qkv(x, w, b, nwq, nwk, cos, sin, M, y)
     # table rows wrapping per sequence, with sampled rows

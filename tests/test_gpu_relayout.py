@@ -150,7 +150,15 @@ def test_fused_prologue_pack_equals_unfused(R, wdtype, heads, world):
     wk = (1 + 0.1 * torch.randn(D, generator=g)).to(wdtype)
     ang = torch.randn((rows, R), generator=g)
     cos, sin = ang.cos(), ang.sin()
-    packed = qknorm_rope_pack_qkv(q, k, v, wq, wk, cos, sin, 1e-5, 1e-6, world)
+    tc, ts = cos, sin
+    if R == 96:
+        # device tables with rows of 98 floats (not 16-byte rows), read in
+        # place: the element-wise kernel in the pack layout
+        tc, ts = torch.zeros((rows, 98), device=DEV), torch.zeros((rows, 98), device=DEV)
+        tc[:, :R], ts[:, :R] = cos.to(DEV), sin.to(DEV)
+        tc, ts = tc[:, :R], ts[:, :R]
+        assert tc.stride(0) == 98
+    packed = qknorm_rope_pack_qkv(q, k, v, wq, wk, tc, ts, 1e-5, 1e-6, world)
     qn, kn = fused_qk_norm_rope(
         q.unsqueeze(0), k.unsqueeze(0), wq.to(DEV), wk.to(DEV), cos.to(DEV), sin.to(DEV), 1e-5, 1e-6
     )
