@@ -65,11 +65,13 @@ constexpr float kSumLimit = 65536.0f;            // row-sum bound of the fast so
 // p of 2^127 * (2 - 2^-8) or more is finite in fp32 but rounds to inf in bf16,
 // and a rescale by 2^-ex with ex > 126 is subnormal; below 2^64 neither occurs.
 constexpr float kRecomputeLimit = 0x1p64f;
-// Rows a K / V buffer resource spans from its base: the main loop rebases
-// both at the first tile of every group of four iterations and loads up to
-// five tiles past the group's last one (tiles j .. j+8 from base j), so
-// 32-bit buffer offsets only ever cover one window of the view, however long
-// the view is.
+// Rows a K / V buffer resource of the wide forms spans from its base: the
+// pipeline prologue loads tiles 0..4 from the view's first tile; the main
+// loop rebases the K resource at the one tile each load reads and moves a
+// token-major V window on every four tiles (loads up to tile j+6 from base
+// j). So 32-bit buffer offsets only ever cover one window of the view,
+// however long the view is. The host accepts a view when kWindowRows of its
+// rows span less than 2^31 bytes.
 constexpr int kWindowRows = kBN * 9;
 constexpr int kPersistMaxQTiles = 16;  // longest segment of a persistent launch: 4,096 rows
 constexpr int kQueuePieces = 4;                  // key-range pieces per tile of a dynamic tail
@@ -130,6 +132,15 @@ __device__ __forceinline__ void wait_vmcnt() {
 // DMA loads in flight are waited for explicitly (wait_vmcnt) before it.
 __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory"); }
 
+// The lane's index within its wave, counted by the hardware (v_mbcnt): a
+// value that can be taken again after a long loop instead of being held in
+// a register across it.
+__device__ __forceinline__ int lane_from_hw() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+}
+
 // One query tile (chunk < 0), or key-range piece `chunk` of `chunks` of a
 // tile. A piece with a workspace slot (slot >= 0) writes normalised fp32
 // partial O and LSE there for the merge; a whole tile, or a piece covering
@@ -137,10 +148,10 @@ __device__ __forceinline__ void barrier() { asm volatile("s_barrier" ::: "memory
 // workgroup call it with the same arguments; it returns with no LDS DMA in
 // flight.
 // kWide: views whose span reaches 2^31 bytes. Their K / V buffer resources
-// are rebased every four key tiles (a window of kWindowRows rows), so 32-bit
-// offsets never cover more than one window. Shorter views keep one resource
-// per view: the rebase needs scalar registers this kernel does not have to
-// spare (the compiler spills them), so it is not paid where it is not needed.
+// are rebased as the key loop moves on (a window of kWindowRows rows), so
+// 32-bit offsets never cover more than one window. Shorter views keep one
+// resource per view: the rebase needs scalar registers this kernel does not
+// have to spare, so it is not paid where it is not needed.
 // kVT: V is read from a d-major copy (p.vt: per (batch, head) 128 rows of
 // keys, zero past the last key), so each PV fragment is one ds_read_b128
 // instead of two transpose reads. The K rows of every 16-key group are then
@@ -167,7 +178,7 @@ template <bool kWide, bool kVT, bool kPersist = false, typename Params>
 __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int chunks, int slot,
                                           bool graded = false, bf16x8* qcarry = nullptr, bool prefetched = false,
                                           int next_tile = -1, const int* cu_cur = nullptr,
-                                          const int* cu_next = nullptr) {
+                                          const int* cu_next = nullptr, int wave_first = 0) {
     static_assert(!kPersist || (!kWide && !kVT), "persistent launches use the narrow token-major form");
     char* const smem = attn_lds();
     // V stages 0..3 first, then K stages 0..3: with a per-lane base in a VGPR
@@ -179,12 +190,15 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
     // Opaque per call, so that no lane-derived value is hoisted out of the
     // piece loop in attn_fwd_kernel and held across it (that cost VGPRs and
     // spills).
-    int tid = threadIdx.x;
+    // The wide forms, short of registers, hold no copy of the work-item id
+    // across calls: wave_first (the wave's first work item, a scalar the
+    // kernel reads once) plus the lane.
+    int tid = kWide ? wave_first + lane_from_hw() : (int)threadIdx.x;
     asm volatile("" : "+v"(tid));
-    const int lane = tid & 63;
+    int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int hi = lane >> 5;  // wave half
-    const int l32 = lane & 31;
+    int hi = lane >> 5;  // wave half
+    int l32 = lane & 31;
     // Key (within a 32-key block) of S^T row r.
     auto krowperm = [](int r) { return kVT ? keyperm(r) : r; };
 
@@ -266,9 +280,9 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
     // the padded key range read the next dim row's keys (finite values that
     // meet P = 0) or, in the last row, zeros.
     i32x4 rv = kVT ? make_rsrc_words(vb, (uint32_t)(kD * p.vt_rs - 2 * (k0 + vpad))) : window(vb, p.v_rs, 0);
-    // Moves a window (kWide) four key tiles on, to start at tile j0: the
-    // 48-bit base of words 0-1 (stride bits zero) grows by 4 * kBN rows; the
-    // range is recomputed from the rows left.
+    // Moves a token-major V window (kWide) four key tiles on, to start at
+    // tile j0: the 48-bit base of words 0-1 (stride bits zero) grows by
+    // 4 * kBN rows; the range is recomputed from the rows left.
     auto advance = [&](i32x4& r, int row_bytes, int j0) {
         const uint64_t base = ((uint64_t)(uint32_t)r.y << 32 | (uint32_t)r.x) + (uint64_t)(4 * kBN) * (uint32_t)row_bytes;
         r.x = (int)(uint32_t)base;
@@ -325,11 +339,16 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
     // buffer_load ... lds writes 16 bytes per lane to LDS address M0 + 16*lane;
     // M0 needs one wait state before the load reads it. Nothing else in this
     // kernel uses M0 (it is a reserved register, so it is not listed as
-    // clobbered). `tile` counts from the current window's first tile.
-    auto dma1 = [&](const i32x4& rsrc, int row_bytes, const uint32_t* lanes, char* stage, int tile, int i) {
+    // clobbered). `tile` counts from the resource's first tile. An opaque
+    // skip (a scalar the compiler cannot fold) is added to the lane offset at
+    // the load itself, where a constant one would have the compiler hold
+    // every (tile, load) sum in its own VGPR.
+    auto dma1 = [&](const i32x4& rsrc, int row_bytes, const uint32_t* lanes, char* stage, int tile, int i,
+                    bool opaque = false) {
         // A tile is kBN rows of row_bytes, or (d-major V, row_bytes 0) 2 * kBN
         // bytes along every dim row.
-        const uint32_t skip = (uint32_t)(tile * (row_bytes != 0 ? kBN * row_bytes : 2 * kBN));
+        uint32_t skip = (uint32_t)(tile * (row_bytes != 0 ? kBN * row_bytes : 2 * kBN));
+        if (opaque) asm volatile("" : "+s"(skip));
         const uint32_t dst = (uint32_t)(uintptr_t)(const lds_char*)(stage + (wave * kDmaPerTile + i) * 4 * kRow);
         asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                      :
@@ -338,7 +357,11 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
     };
     // Load i (of kDmaPerTile) of this wave's share of a K / V tile.
     auto dma_k1 = [&](int tile, int stage, int i) { dma1(rk, p.k_rs, dk, kst + stage * kTile, tile, i); };
-    auto dma_v1 = [&](int tile, int stage, int i) { dma1(rv, kVT ? 0 : p.v_rs, dv, vst + stage * kTile, tile, i); };
+    // (The token-major V of the wide forms is addressed per window of four
+    // tiles, with opaque skips.)
+    auto dma_v1 = [&](int tile, int stage, int i) {
+        dma1(rv, kVT ? 0 : p.v_rs, dv, vst + stage * kTile, tile, i, kWide && !kVT);
+    };
     auto dma_k = [&](int tile, int stage) {
 #pragma unroll
         for (int i = 0; i < kDmaPerTile; ++i) dma_k1(tile, stage, i);
@@ -719,26 +742,25 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
         constexpr int U = decltype(u)::value;
         constexpr bool kTail = decltype(tail_c)::value;
         static_assert(!kTail || U >= 2, "only the last two steps of a group skip QK^T");
-        // A group of four iterations starts at tile jj: rebase the K / V
-        // windows there. Its iterations load K up to tile jj+8 and V up to
-        // jj+6, inside the window's kWindowRows.
-        if constexpr (kWide && U == 0) {
-            if (jj > 0) {
-                advance(rk, p.k_rs, jj);
-                if constexpr (!kVT) advance(rv, p.v_rs, jj);
-            }
+        // Iteration jj loads K tile jj+5 and V tile jj+3. The wide forms
+        // rebase the K resource at that tile every iteration (scalar work
+        // only), so each K load takes its lane offset as it is, and move a
+        // token-major V window on at the first iteration of every group of
+        // four (its loads, tiles jj+3 .. jj+6, stay inside the window). The
+        // d-major V resource is never rebased.
+        if constexpr (kWide && !kTail) rk = window(kb, p.k_rs, jj + 5);
+        if constexpr (kWide && !kVT && U == 0) {
+            if (jj > 0) advance(rv, p.v_rs, jj);
         }
-        // Tile numbers of the DMA: counted from the window's first tile, jj - U
-        // (kWide), or from the view's first tile.
-        const int jt = kWide ? U : jj;
-        const int jv = kWide && !kVT ? U : jj;  // the d-major V resource is never rebased
+        const int kt = kWide ? 0 : jj + 5;
+        const int vt = kWide && !kVT ? U + 3 : jj + 3;
         // The four loads are spread over the iteration so that their LDS
         // writes do not arrive as one burst that holds up the fragment reads.
         auto hook = [&](int k) __attribute__((always_inline)) {
-            if (k == 0) dma_k1(jt + 5, (U + 1) & 3, 0);
-            if (k == 8) dma_k1(jt + 5, (U + 1) & 3, 1);
-            if (k == 16) dma_v1(jv + 3, (U + 3) & 3, 0);
-            if (k == 24) dma_v1(jv + 3, (U + 3) & 3, 1);
+            if (k == 0) dma_k1(kt, (U + 1) & 3, 0);
+            if (k == 8) dma_k1(kt, (U + 1) & 3, 1);
+            if (k == 16) dma_v1(vt, (U + 3) & 3, 0);
+            if (k == 24) dma_v1(vt, (U + 3) & 3, 1);
         };
         if constexpr (kTail) {
             constexpr std::integral_constant<int, U == 2 ? 1 : 0> sm{};
@@ -772,6 +794,13 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
         step(std::integral_constant<int, 2>{}, j + 2, std::false_type{});
         step(std::integral_constant<int, 3>{}, j + 3, std::false_type{});
     }
+    if constexpr (kWide) {
+        // Take the lane again for the last steps and the epilogue rather
+        // than hold it across the key loop.
+        lane = lane_from_hw();
+        hi = lane >> 5;
+        l32 = lane & 31;
+    }
     if (nsteps > 0) {
         step(std::integral_constant<int, 0>{}, j, std::false_type{});
         step(std::integral_constant<int, 1>{}, j + 1, std::false_type{});
@@ -787,6 +816,9 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
     }
     const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
     const float lse = l_run > 0.f ? (mc + __log2f(l_run)) * 0.69314718055994531f : -INFINITY;
+    // Query row of the lane: the wide forms take it from the lane taken
+    // after the key loop rather than hold it across the loop.
+    const int emq = kWide ? m0 + wave * 32 + l32 : mq;
     if (slot >= 0) {
         // Partial result of a key-range piece: normalised O in bf16 (as the
         // output itself is rounded) and the LSE in fp32.
@@ -805,8 +837,8 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
         if (hi == 0) p.ws_lse[(int64_t)slot * kBM + row] = lse;
         return false;
     }
-    if (mq < sq) {
-        char* ob = (char*)p.o + 2 * (b * p.o_sb + h * p.o_sh) + (int64_t)(q0 + mq) * p.o_rs;
+    if (emq < sq) {
+        char* ob = (char*)p.o + 2 * (b * p.o_sb + h * p.o_sh) + (int64_t)(q0 + emq) * p.o_rs;
 #pragma unroll
         for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -817,7 +849,7 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
                 w.y = (int)pack_bf16x2(oacc[db][i * 4 + 2] * inv, oacc[db][i * 4 + 3] * inv);
                 *(i32x2*)(ob + d * 2) = w;
             }
-        if (p.lse != nullptr && hi == 0) p.lse[b * p.lse_sb + h * p.lse_sh + q0 + mq] = lse;
+        if (p.lse != nullptr && hi == 0) p.lse[b * p.lse_sb + h * p.lse_sh + q0 + emq] = lse;
     }
     return pref;
 }
@@ -845,6 +877,8 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // XCDs nearly only empty tiles: the 49,920 + 1,296 two-segment batch ran
     // at half speed).
     const int bid = blockIdx.x;
+    // First work item of this wave (wide forms: read once, kept as a scalar).
+    const int wave_first = kWide ? __builtin_amdgcn_readfirstlane((int)threadIdx.x) & ~63 : 0;
     int tile = bid, chunk = -1, chunks = 1, slot = -1;
     const bool planned = p.vplan != nullptr;
     // With a tail queue, the workgroups after the whole tiles take the pieces
@@ -877,12 +911,15 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
     // code (a single call inside the loop below changed its register
     // allocation and made it 1-2% slower).
     if (!queued) {
-        attn_tile<kWide, kVT>(p, tile, chunk, chunks, slot);
+        attn_tile<kWide, kVT>(p, tile, chunk, chunks, slot, false, nullptr, false, -1, nullptr, nullptr, wave_first);
         return;
     }
     int* const counter = planned ? (int*)p.vplan + kPlanQueue : p.queue;
+    // The wide forms find the first work item from wave_first and the lane,
+    // so no VGPR holds the id across the loop.
+    const bool leader = kWide ? wave_first + lane_from_hw() == 0 : threadIdx.x == 0;
     for (;;) {
-        if (threadIdx.x == 0) queue_head = atomicAdd(counter, 1);
+        if (leader) queue_head = atomicAdd(counter, 1);
         __syncthreads();  // also: every wave is done with the previous piece's LDS
         const int piece = __builtin_amdgcn_readfirstlane(queue_head);  // uniform: keep it scalar
         __syncthreads();  // every wave has read queue_head before it is written again
@@ -912,7 +949,7 @@ __global__ __launch_bounds__(kThreads, 2) void attn_fwd_kernel(AttnParams p) {
         int zero;
         asm volatile("s_mov_b32 %0, 0" : "=s"(zero));
         KernArgs* pk = (KernArgs*)((const __attribute__((address_space(4))) char*)&p + zero);
-        attn_tile<kWide, kVT>(*pk, tile, chunk, chunks, slot, !planned);
+        attn_tile<kWide, kVT>(*pk, tile, chunk, chunks, slot, !planned, nullptr, false, -1, nullptr, nullptr, wave_first);
     }
 }
 

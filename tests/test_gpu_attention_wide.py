@@ -3,7 +3,7 @@
 The reference's seam hands the kernel ``to_qkv(...).chunk(3)`` views of any
 length (src/h3_flash/runtime/attention/dense_fa4.py:123-131,145). Views whose
 rows span 2^31 bytes or more take the kernel's wide form, whose K / V buffer
-resources are rebased per window of key tiles. The narrow form runs the same
+resources are rebased at every key tile they load. The narrow form runs the same
 tiles in the same order on a contiguous copy, so both must give the same
 bits; sampled rows are also checked against the CPU oracle.
 """
@@ -79,3 +79,26 @@ def test_views_past_4gib_dense_split_and_varlen():
     torch.cuda.synchronize()
     assert torch.equal(out, out_c) and torch.equal(lse, lse_c)
     _check_rows(qc, kc, vc, out, lse, torch.tensor([0, 17_000, 17_001, 30_000, S - 1]), cu=cu.cpu(), tag="varlen")
+
+
+def test_short_key_views_past_2gib_token_major_v():
+    """Eight heads of q, k and v as column slices of a (12,000, 8, 16,384)
+    buffer: 256 KiB rows, a 3.15 GB span. Under 16,384 keys the kernel reads
+    V token-major (no d-major copy), so this is the wide form's other V
+    layout; 376 tiles: one whole round on the chip, the rest as key-range
+    pieces from the counter."""
+
+    S, H, W, D = 12_000, 8, 1 << 14, 128
+    print(f"case: token-major V column views S={S} H={H} row stride {H * W}", flush=True)
+    buf = torch.empty((1, S, H, W), dtype=torch.bfloat16, device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(47)
+    buf[..., : 3 * D] = torch.randn((1, S, H, 3 * D), device=DEV, generator=g).to(torch.bfloat16)
+    q, k, v = buf[..., :D], buf[..., D : 2 * D], buf[..., 2 * D : 3 * D]
+    assert q.stride(1) * 2 * S >= 2**31
+    qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+    out, lse = flash_attn_func(q, k, v)
+    out_c, lse_c = flash_attn_func(qc, kc, vc)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_c) and torch.equal(lse, lse_c)
+    del buf, q, k, v
+    _check_rows(qc, kc, vc, out, lse, torch.tensor([0, 255, 256, 6_000, S - 33, S - 1]), tag="token-major V")
