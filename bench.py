@@ -148,8 +148,8 @@ def wide_view_rates(torch, heads: int = 40, seqlen: int = 72003, head_dim: int =
     buffer, the form the reference's processor hands the kernel
     (dense_fa4.py:123-131,145), at a length where a view's rows span 2^31
     bytes or more (40 heads: beyond about 69,000 tokens), so the kernel runs
-    its wide form (buffer resources rebased per query tile and per window of
-    keys); next to the same q, k, v as contiguous tensors (the narrow form),
+    its wide form (buffer resources rebased per query tile and as the key
+    loop moves on); next to the same q, k, v as contiguous tensors (the narrow form),
     on the same inputs. Outputs must be bit-identical."""
 
     from h3_flash_amd import flash_attn_func

@@ -186,6 +186,8 @@ def qkv_projection(
     wq_n, wk_n = getattr(nq, "weight", None), getattr(nk, "weight", None)
     if not (isinstance(wq_n, torch.Tensor) and isinstance(wk_n, torch.Tensor)):
         return no("norm_q / norm_k carry no weight")
+    if getattr(nq, "eps", None) is None or getattr(nk, "eps", None) is None:
+        return no("norm_q / norm_k carry no eps")
     if wq_n.shape != (HEAD_DIM,) or wk_n.shape != (HEAD_DIM,) or wq_n.dtype != torch.bfloat16 or wk_n.dtype != torch.bfloat16:
         return no("norm weights are not bf16 of head_dim 128")
     if attn.fused_projections:

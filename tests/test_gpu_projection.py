@@ -340,3 +340,14 @@ def test_fallbacks_are_recorded_in_the_install_audit():
     assert fb["no rotary_emb: the module's own norms apply"] == 2
     assert sum(v for k, v in fb.items() if k.startswith("rotary tables of shape (64, 7)")) == 1
     assert qkv_projection(t.blocks[0], x, None) is None  # the module's own norms apply without RoPE
+    # norms without an eps (torch's RMSNorm(eps=None)): the fused launch
+    # declines with the reason, and the separate steps then refuse the module
+    # with their own message, as for any norm they cannot fuse
+    blk = t.blocks[1]
+    blk.norm_k.eps = None
+    why: list[str] = []
+    assert qkv_projection(blk, x, (cos, sin), why) is None
+    assert why == ["norm_q / norm_k carry no eps"]
+    with torch.no_grad(), pytest.raises(RuntimeError, match="needs norm_q/norm_k"):
+        blk(x, rotary_emb=(cos, sin))
+    assert record["projection_fallbacks"]["norm_q / norm_k carry no eps"] == 1
