@@ -8,7 +8,7 @@ HIP prologue, v is N(0,1). A step is one attention forward over that batch;
 TFLOP/s = 4 * S^2 * D * H / t.
 
 Prints one JSON line with the metric, the kernel's roofline position (HIP
-events around every timed launch on the launch stream), the prologue's HBM
+events around the timed launches on the launch stream), the prologue's HBM
 rate, and the reference's CPU path (torch SDPA on host bf16 tensors, the call
 form of benchmarks/benchmark_dense_fa4.py:70-77) timed on a bounded sample of
 query rows on this host's cores.
@@ -659,19 +659,18 @@ def main(argv=None) -> int:
         step()
     torch.cuda.synchronize()
 
-    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
     region0 = torch.cuda.Event(enable_timing=True)
     region1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     # Per-CU cycle counters just outside the timed region (one small launch
     # on each side): the core clock the part held over the timed launches.
+    # The region holds the K calls and nothing else: two timing events per
+    # call inside it measured 0.2% of a C2 call on the GPU's timeline.
     clock0 = devclock.sample(torch, dev)
     wall0 = time.perf_counter()
     region0.record(stream)
-    for a, b in events:
-        a.record(stream)
+    for _ in range(args.steps):
         step()
-        b.record(stream)
     region1.record(stream)
     clock1 = devclock.sample(torch, dev)
     torch.cuda.synchronize()
@@ -679,9 +678,19 @@ def main(argv=None) -> int:
     sclk = clock.get("sclk_mhz")
     wall = time.perf_counter() - wall0
     region_ms = region0.elapsed_time(region1)
-    launch_ms = [a.elapsed_time(b) for a, b in events]
     ms_per_step = region_ms / args.steps
-    kernel_ms = statistics.fmean(launch_ms)
+    # The call's mean duration over the timed region (HIP events on the
+    # launch stream): vt + attention + merge kernels and the gaps between.
+    kernel_ms = ms_per_step
+    # The spread of single calls, from a second pass of the same K calls
+    # with an event pair around each (not part of the figures above).
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    for a, b in events:
+        a.record(stream)
+        step()
+        b.record(stream)
+    torch.cuda.synchronize()
+    launch_ms = [a.elapsed_time(b) for a, b in events]
 
     peak_memory = torch.cuda.max_memory_allocated(dev)
     flops = w.flops
@@ -737,14 +746,16 @@ def main(argv=None) -> int:
             "traffic": traffic,
             "traffic_source": traffic_source,
             "kernel": "attn_fwd_kernel",
-            # events around each call: for dense launches with more tiles than
-            # CUs that is attn_vt_kernel (d-major V copy; it also zeroes the
-            # tail's counter) + attn_fwd_kernel + attn_merge_kernel (the tail's
-            # pieces), all of them part of the attention
+            # the call over the timed region: for dense launches with more
+            # tiles than CUs that is attn_vt_kernel (d-major V copy; it also
+            # zeroes the tail's counter) + attn_fwd_kernel + attn_merge_kernel
+            # (the tail's pieces), all of them part of the attention
             "kernel_ms_scope": "whole flash_attn_func call on its stream: attn_vt_kernel (d-major V copy), "
-            "attn_fwd_kernel, attn_merge_kernel (the tail's pieces)",
+            "attn_fwd_kernel, attn_merge_kernel (the tail's pieces); mean over the timed region; min and "
+            "median of single calls from a second pass with events around each call",
             "kernel_ms_mean": kernel_ms,
             "kernel_ms_min": min(launch_ms),
+            "kernel_ms_median_single": statistics.median(launch_ms),
             "algorithmic_flop_per_launch": flops,
             "compulsory_hbm_bytes_per_launch": compulsory,
         },
