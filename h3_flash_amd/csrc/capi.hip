@@ -49,6 +49,9 @@ int prepare_attn(const h3a_attn_args* a, h3a::AttnParams& p, bool* empty) {
                     (long long)a->batch, (long long)a->heads, (long long)a->seqlen_q, (long long)a->seqlen_k);
     if (!(a->softmax_scale > 0.f) || !isfinite(a->softmax_scale))
         return fail(H3A_EINVAL, "h3a_attn_fwd: softmax_scale must be finite and > 0");
+    // The launch description holds these in 32 bits.
+    if (a->batch > INT32_MAX || a->heads > INT32_MAX)
+        return fail(H3A_EUNSUPPORTED, "h3a_attn_fwd: batch and heads must be below 2^31");
     if (a->batch == 0 || a->seqlen_q == 0) {
         *empty = true;
         return H3A_OK;
@@ -666,8 +669,10 @@ int h3a_attn_merge(const h3a_attn_merge_args* a, void* stream) {
     if ((!pf && a->part_dtype != H3A_DTYPE_BF16) || (!of && a->out_dtype != H3A_DTYPE_BF16))
         return fail(H3A_EINVAL, "%s: part and out dtypes must be bf16 or fp32", fn);
     if (a->batch == 0 || a->seqlen == 0) return H3A_OK;
-    if ((__int128)a->batch * a->seqlen * a->heads >= ((int64_t)1 << 40))
-        return fail(H3A_EUNSUPPORTED, "%s: too many rows", fn);
+    if ((__int128)a->batch * a->seqlen * a->heads >= ((int64_t)1 << 40) || a->heads >= ((int64_t)1 << 31) ||
+        a->seqlen >= ((int64_t)1 << 31))
+        return fail(H3A_EUNSUPPORTED, "%s: too many rows (batch x seqlen x heads under 2^40, heads and seqlen under 2^31)",
+                    fn);
     if (!a->o) return fail(H3A_EINVAL, "%s: NULL output", fn);
     const int64_t psz = pf ? 4 : 2, osz = of ? 4 : 2;
     h3a::AttnMergeParams p{};
@@ -696,8 +701,6 @@ int h3a_attn_merge(const h3a_attn_merge_args* a, void* stream) {
     p.heads = (int32_t)a->heads; p.seqlen = (int32_t)a->seqlen; p.head_dim = (int32_t)a->head_dim;
     p.rows = a->batch * a->seqlen * a->heads;
     p.part_f32 = pf; p.out_f32 = of;
-    if (a->seqlen >= ((int64_t)1 << 31) || a->heads >= ((int64_t)1 << 31))
-        return fail(H3A_EUNSUPPORTED, "%s: seqlen and heads must be < 2^31", fn);
     hipError_t e = h3a::launch_attn_merge(p, (hipStream_t)stream);
     if (e != hipSuccess) return fail(H3A_ELAUNCH, "%s: launch failed: %s", fn, hipGetErrorString(e));
     return H3A_OK;

@@ -250,7 +250,7 @@ struct ProjGemmParams {
     int32_t m_tiles, n_tiles;  // n_tiles = sum of the sections' tiles
     int32_t n_sections;
     ProjSection sec[kProjMaxSections];
-    const float* cos;  // fp32 (seqlen, table_stride) rotate-half tables (mode-1 sections with rotary_dim > 0)
+    const float* cos;  // fp32 (seqlen, table_stride) tables (norm sections with rotary_dim > 0)
     const float* sin;
     int64_t table_stride;
     int32_t rotary_dim;

@@ -103,6 +103,9 @@ def _attn_args(**overrides):
         ({"k_stride": (ctypes.c_int64 * 3)(1 << 62, 1 << 61, 128)}, _ext.H3A_EUNSUPPORTED, "row stride"),
         ({"lse": (1 << 20) + 2}, _ext.H3A_EINVAL, "lse must be 4-byte aligned"),
         ({"lse": 1 << 20, "lse_stride": (ctypes.c_int64 * 2)(-16, 16)}, _ext.H3A_EINVAL, "non-negative strides"),
+        # extents that 32-bit launch fields would truncate
+        ({"heads": (1 << 32) + 1}, _ext.H3A_EUNSUPPORTED, "below 2^31"),
+        ({"batch": 1 << 31}, _ext.H3A_EUNSUPPORTED, "below 2^31"),
     ],
 )
 @host_only
@@ -416,6 +419,9 @@ def _attn_merge_args(**overrides):
         ({"o": None}, _ext.H3A_EINVAL, "NULL output"),
         ({"o": (1 << 24) + 8}, _ext.H3A_EINVAL, "aligned"),
         ({"batch": 1 << 30, "seqlen": 1 << 30, "heads": 1 << 30}, _ext.H3A_EUNSUPPORTED, "too many rows"),
+        # under 2^40 rows, but one extent past the 32-bit launch fields
+        ({"seqlen": 1 << 33, "heads": 1}, _ext.H3A_EUNSUPPORTED, "too many rows"),
+        ({"heads": 1 << 32, "seqlen": 2}, _ext.H3A_EUNSUPPORTED, "too many rows"),
     ],
 )
 @host_only
