@@ -89,9 +89,11 @@ def merge_attention(
         # parts of one call share a dtype), so nothing is rounded twice.
         k = _ext.H3A_MERGE_MAX_PARTS
         head = merge_attention(outs[:k], lses[:k], out_dtype=torch.float32)
+        # the output dtype as a call with 16 parts or fewer picks it
+        final_dtype = out_dtype or (out.dtype if out is not None else outs[0].dtype)
         return merge_attention(
             [head[0], *(o.float() for o in outs[k:])], [head[1], *lses[k:]],
-            out=out, lse=lse, out_dtype=out_dtype or outs[0].dtype,
+            out=out, lse=lse, out_dtype=final_dtype,
         )
     ref = outs[0]
     if ref.dim() != 4 or not ref.is_cuda:

@@ -87,6 +87,11 @@ def test_merge_more_than_sixteen_parts_and_in_place():
     ro, rl = merge_reference(outs, lses)
     o, l = merge_attention([x.to(DEV) for x in outs], [x.to(DEV) for x in lses])
     assert_parity(o, ro.to(torch.bfloat16), "merge21")
+    # a caller's fp32 output takes the dtype from it, as with 16 parts or fewer
+    o32 = torch.empty(outs[0].shape, dtype=torch.float32, device=DEV)
+    got, _ = merge_attention([x.to(DEV) for x in outs], [x.to(DEV) for x in lses], out=o32)
+    assert got.data_ptr() == o32.data_ptr() and got.dtype == torch.float32
+    assert (got.cpu() - ro).abs().max().item() <= 2e-3
     # in place: out and lse alias part 0
     d_outs = [x.to(DEV) for x in outs[:4]]
     d_lses = [x.to(DEV) for x in lses[:4]]
