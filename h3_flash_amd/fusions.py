@@ -71,8 +71,10 @@ def _tables(tables: list[torch.Tensor], columns: int, device: torch.device) -> l
         out.append(t.to(device))
     dtype = torch.bfloat16 if all(t.dtype == torch.bfloat16 for t in out) else torch.float32
     out = [t.to(dtype) for t in out]
-    # _row_addressable (fusions.py:190-191): the last dimension must be contiguous
-    return [t if t.stride(-1) == 1 else t.contiguous() for t in out]
+    # _row_addressable (fusions.py:190-191): the last dimension must be
+    # contiguous; broadcast rows (a row stride under the row, e.g. expand())
+    # are written out, since the launch takes one row stride per table
+    return [t if t.stride(-1) == 1 and t.stride(0) >= columns else t.contiguous() for t in out]
 
 
 def _index(index: torch.Tensor, device: torch.device) -> torch.Tensor:

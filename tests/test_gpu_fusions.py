@@ -123,6 +123,25 @@ def test_strided_rows_and_clamped_index():
     assert_parity(got, rmsnorm_modulate_reference(x, weight, scale, shift, index, 1e-5), "strided")
 
 
+def test_broadcast_table_rows():
+    # modulation tables whose rows are one row broadcast on the device
+    # (expand: row stride 0)
+    rows, hidden = 24, 2048
+    x, branch, weight, (shift, scale, gate, _, _, _) = _inputs(rows, hidden, seed=9)
+    one = lambda t: t[:1].expand(9, hidden)  # noqa: E731
+    dev1 = lambda t: t[:1].to(DEV).expand(9, hidden)  # noqa: E731
+    assert dev1(scale).stride(0) == 0
+    index = torch.arange(rows, dtype=torch.int64) % 9
+    got = fused_rmsnorm_modulate(x.to(DEV), weight.to(DEV), dev1(scale), dev1(shift), index.to(DEV), 1e-5)
+    assert_parity(got, rmsnorm_modulate_reference(x, weight, one(scale), one(shift), index, 1e-5), "broadcast")
+    h, n = fused_residual_gate_rmsnorm_modulate(
+        x.to(DEV), branch.to(DEV), dev1(gate), weight.to(DEV), dev1(scale), dev1(shift), index.to(DEV), 1e-5
+    )
+    rh, rn = residual_gate_rmsnorm_modulate_reference(x, branch, one(gate), weight, one(scale), one(shift), index, 1e-5)
+    assert_parity(h, rh, "broadcast hidden")
+    assert_parity(n, rn, "broadcast normed")
+
+
 @pytest.mark.parametrize("rows, ffn", [(257, 14336), (6240, 14336), (7, 1000), (5, 1001)])
 def test_swiglu(rows, ffn):
     x = (torch.randn((rows, 2 * ffn), generator=torch.Generator().manual_seed(ffn)) * 3).to(torch.bfloat16)
