@@ -51,7 +51,9 @@ def _table(t: torch.Tensor, seqlen: int, device: torch.device) -> torch.Tensor:
     if t.dim() != 2 or t.shape[0] != seqlen:
         raise ValueError(f"cos/sin tables must be (seq={seqlen}, rotary_dim), got {tuple(t.shape)}")
     t = t.to(device=device, dtype=torch.float32)
-    return t if t.stride(-1) == 1 else t.contiguous()
+    # broadcast rows (a row stride under the row, e.g. expand()) are written
+    # out: the launch reads row s at s * table_stride with table_stride >= R
+    return t if t.stride(-1) == 1 and t.stride(0) >= t.shape[-1] else t.contiguous()
 
 
 def _tables(cos: torch.Tensor, sin: torch.Tensor, seqlen: int, device: torch.device):

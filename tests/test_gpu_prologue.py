@@ -118,6 +118,20 @@ def test_cos_and_sin_with_different_row_strides():
     assert_rounding_parity(ok, expect, "k")
 
 
+def test_broadcast_table_rows():
+    # one table row broadcast over the sequence on the device (expand: row
+    # stride 0), as a caller may pass for a single position
+    B, S, H, D, R = 1, 24, 2, 128, 64
+    x = _rand((B, S, H, D), 10)
+    w = torch.ones(D, dtype=torch.bfloat16)
+    ang = torch.randn((1, R), generator=torch.Generator().manual_seed(11))
+    cos_d, sin_d = ang.cos().to(DEV).expand(S, R), ang.sin().to(DEV).expand(S, R)
+    assert cos_d.stride(0) == 0
+    expect = qknorm_rope_reference(x, w, ang.cos().expand(S, R), ang.sin().expand(S, R), 1e-5)
+    y = fused_qknorm_rope(x.to(DEV), w.to(DEV), cos_d, sin_d, 1e-5)
+    assert_rounding_parity(y, expect, "broadcast")
+
+
 @pytest.mark.parametrize("name", ["c2", "c5"])
 def test_full_size_workload(name):
     raw = make_raw(WORKLOADS[name])
