@@ -96,7 +96,12 @@ extern "C" {
  * 2^31 bytes: a sequence stride under 1,864,136 elements; larger strides
  * return H3A_EUNSUPPORTED. Views whose rows plus an 896-row margin reach
  * 2^31 bytes run in a form of the kernel that rebases its buffer resources
- * per query tile and per 576-row window of keys.
+ * per query tile and as the key loop moves on (each within a 576-row
+ * window).
+ *
+ * Extents: batch and heads below 2^31, seqlen_q and seqlen_k below 2^30, and
+ * at most 2^31 - 1 query tiles (256 rows of one head) in all; larger ones
+ * return H3A_EUNSUPPORTED (sequence lengths: H3A_EINVAL).
  *
  * Workspace: h3a_attn_fwd_workspace_size(args) bytes of device memory at
  * `workspace` (256-byte aligned, contents on entry irrelevant), used for:
