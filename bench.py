@@ -759,7 +759,15 @@ def main(argv=None) -> int:
             "algorithmic_flop_per_launch": flops,
             "compulsory_hbm_bytes_per_launch": compulsory,
         },
-        "prologue": prologue,
+        # the q/k prologue timed on its own (its HBM rate above) and the
+        # prologue + attention sum, as one H3 block runs them back to back
+        "prologue": None
+        if prologue is None
+        else {
+            **prologue,
+            "prologue_plus_attention_ms": prologue["ms"] + ms_per_step,
+            "prologue_plus_attention_TFLOP_s": flops / ((prologue["ms"] + ms_per_step) * 1e-3) / 1e12,
+        },
         "peak_gpu_memory_bytes": peak_memory,
         "workspace_bytes": workspace_bytes(q, k, v, out, lse, kw),
         "wall_s_timed_region": wall,
