@@ -102,3 +102,56 @@ def test_short_key_views_past_2gib_token_major_v():
     assert torch.equal(out, out_c) and torch.equal(lse, lse_c)
     del buf, q, k, v
     _check_rows(qc, kc, vc, out, lse, torch.tensor([0, 255, 256, 6_000, S - 33, S - 1]), tag="token-major V")
+
+
+@pytest.mark.parametrize(
+    "S, H, W",
+    [(40_000, 1, 1 << 16), (12_000, 8, 1 << 14)],
+    ids=["d-major-V-5GB-rows", "token-major-V-3GB-rows"],
+)
+def test_wide_forms_on_extreme_scores(S, H, W):
+    """The softmax's offset raise and overflow recompute in the wide forms
+    (whose overflow path reloads K through a resource at the tile's first
+    row): random scores at softmax_scale 12, and one key 100 log2 units
+    above the rest, on column views whose rows span 3 GB and more, bit-equal
+    to the narrow form on contiguous copies and within the extreme-scale
+    bounds of the oracle on sampled rows."""
+
+    import numpy as np
+
+    D = 128
+    buf = torch.empty((1, S, H, W), dtype=torch.bfloat16, device=DEV)
+    q, k, v = buf[..., :D], buf[..., D : 2 * D], buf[..., 2 * D : 3 * D]
+    assert q.stride(1) * 2 * S >= 2**31
+    g = torch.Generator(device=DEV).manual_seed(53)
+    rows = torch.unique(torch.cat((torch.randperm(S, generator=torch.Generator().manual_seed(54))[:96],
+                                   torch.tensor([0, 255, 256, S - 1]))))
+    excess = 100.0
+    far = excess / (88.5 * 1.4426950408889634)
+    c = np.float32(np.float32(far) * np.float32(1.4426950408889634))
+    assert abs(float(np.float32(np.float32(88.5) * c)) - excess) < 1e-3
+    for mode, scale in (("random", 12.0), ("far key", far)):
+        print(f"case: wide S={S} H={H} row stride {H * W} {mode}", flush=True)
+        if mode == "random":
+            buf[..., : 3 * D] = torch.randn((1, S, H, 3 * D), device=DEV, generator=g).to(torch.bfloat16)
+        else:
+            buf[..., : 2 * D] = 0
+            buf[..., 0] = 1.0  # every query is e0
+            buf[:, S // 3, :, D] = 88.5  # one key far above the rest
+        qc, kc, vc = q.contiguous(), k.contiguous(), v.contiguous()
+        out, lse = flash_attn_func(q, k, v, softmax_scale=scale)
+        out_c, lse_c = flash_attn_func(qc, kc, vc, softmax_scale=scale)
+        torch.cuda.synchronize()
+        assert torch.equal(out, out_c) and torch.equal(lse, lse_c), mode
+        ref_o, ref_l = sdpa_rows(qc.cpu(), kc.cpu(), vc.cpu(), rows, scale)
+        idx = rows.to(DEV)
+        m = error_metrics(out[:, idx].float().cpu(), ref_o)
+        peak = max(ref_o.abs().max().item(), 1.0)
+        l = lse[:, :, idx].double().cpu()
+        lse_err = ((l - ref_l.double()).abs() - 1e-6 * ref_l.double().abs()).max().item()
+        assert m["finite"], mode
+        assert m["max_abs"] <= max(ATTN_MAX_ABS, 2**-6 * peak), (mode, m)
+        assert lse_err <= LSE_MAX_ABS, (mode, lse_err)
+        if mode == "random":
+            assert m["relative_l2"] <= 4e-3 and m["cosine"] >= 0.99999, (mode, m)
+        del qc, kc, vc
