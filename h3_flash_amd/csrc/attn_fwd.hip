@@ -448,6 +448,9 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
         }
     };
 
+    // Persistent launches: set once this tile has issued the next tile's
+    // loads, Q into qf included (its last two iterations).
+    bool pref = false;
     // Redo the softmax of a tile whose row sum passed kRecomputeLimit: S again from
     // K in global memory (its LDS stage may already hold a newer tile) and
     // the resident Q, then the exact max of the tile, a new offset at or
@@ -460,12 +463,31 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
         const auto rk_tile =
             kWide ? make_rsrc(kb + (int64_t)first * p.k_rs, span_bytes(min(sk - first, kBN), p.k_rs)) : rk_plain;
         f32x16 s2[2] = {f32x16{}, f32x16{}};
+        bool q_resident = true;
+        if constexpr (kPersist) q_resident = !pref;
+        if (q_resident) {
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            const uint32_t row = (uint32_t)(tile * kBN - first + 32 * (t & 1) + krow);
-            const i32x4 raw = buf_load16(rk_tile, row * (uint32_t)p.k_rs + (t >> 1) * 32 + hi * 16);
-            s2[t & 1] =
-                __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, raw), qf[t >> 1], s2[t & 1], 0, 0, 0);
+            for (int t = 0; t < 16; ++t) {
+                const uint32_t row = (uint32_t)(tile * kBN - first + 32 * (t & 1) + krow);
+                const i32x4 raw = buf_load16(rk_tile, row * (uint32_t)p.k_rs + (t >> 1) * 32 + hi * 16);
+                s2[t & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, raw), qf[t >> 1],
+                                                                    s2[t & 1], 0, 0, 0);
+            }
+        } else if constexpr (kPersist) {
+            // The last softmax of a persistent tile runs after qf took the
+            // next tile's Q: this tile's Q fragments come from memory again.
+            const __amdgpu_buffer_rsrc_t rq_cur = make_rsrc(qb, span_bytes(sq, p.q_rs));
+#pragma unroll
+            for (int ks = 0; ks < 8; ++ks) {
+                const bf16x8 qk = __builtin_bit_cast(bf16x8, buf_load16(rq_cur, (uint32_t)(mq * p.q_rs + ks * 32 + hi * 16)));
+#pragma unroll
+                for (int t = 2 * ks; t < 2 * ks + 2; ++t) {
+                    const uint32_t row = (uint32_t)(tile * kBN - first + 32 * (t & 1) + krow);
+                    const i32x4 raw = buf_load16(rk_tile, row * (uint32_t)p.k_rs + ks * 32 + hi * 16);
+                    s2[t & 1] =
+                        __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, raw), qk, s2[t & 1], 0, 0, 0);
+                }
+            }
         }
         if ((tile + 1) * kBN > sk) mask_tail(s2[0], s2[1], tile);
         float mx = s2[0][0];
@@ -696,7 +718,6 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
     // past-end DMA of this tile land before the same rows are written again.
     // The Q loads are compiler builtins, so the compiler waits for them
     // before any use or copy of their registers.
-    bool pref = false;
     i32x4 nrv{};
     auto prefetch = [&]() __attribute__((always_inline)) {
         if constexpr (kPersist) {

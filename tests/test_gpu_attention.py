@@ -568,6 +568,37 @@ def test_persistent_short_segments_match_dispatch_order(seed, n_seg, max_len):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("scale", [12.0, 60.0])
+def test_persistent_short_segments_on_extreme_scores(scale):
+    """The persistent launch's softmax offset raise and overflow recompute
+    (random scores at large scales, in tiles that carry a prefetched next
+    tile): bit for bit equal to one workgroup per tile, and sampled segments
+    within the extreme-scale bounds of the oracle."""
+    g = torch.Generator().manual_seed(int(scale))
+    n_seg, H = 120, 2
+    lens = torch.randint(1, 1500, (n_seg,), generator=g)
+    cu = torch.zeros(n_seg + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lens, 0)
+    S = int(cu[-1])
+    q, k, v = (_rand((1, S, H, 128), 70 + i).to(DEV) for i in range(3))
+    kw = dict(cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV), max_seqlen_q=int(lens.max()), softmax_scale=scale)
+    o_p, l_p = flash_attn_func(q, k, v, **kw)
+    o_d, l_d = flash_attn_func(q, k, v, split_tail=False, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o_p, o_d) and torch.equal(l_p, l_d)
+    for s in (0, n_seg // 2, n_seg - 1):
+        a, b = int(cu[s]), int(cu[s + 1])
+        ref_o, ref_l = sdpa_reference(q[:, a:b].cpu(), k[:, a:b].cpu(), v[:, a:b].cpu(), scale)
+        m = error_metrics(o_p[:, a:b].float().cpu(), ref_o)
+        peak = max(ref_o.abs().max().item(), 1.0)
+        lse_err = ((l_p[..., a:b].double().cpu() - ref_l.double()).abs() - 1e-6 * ref_l.double().abs()).max().item()
+        assert m["finite"], (scale, s)
+        assert m["max_abs"] <= max(ATTN_MAX_ABS, 2**-6 * peak), (scale, s, m)
+        assert m["relative_l2"] <= 4e-3 and m["cosine"] >= 0.99999, (scale, s, m)
+        assert lse_err <= LSE_MAX_ABS, (scale, s, lse_err)
+
+
+@pytest.mark.gpu
 def test_persistent_cross_segments_with_empty_key_ranges():
     """Packed cross attention on the persistent launch: query and key
     segments of different lengths, some key ranges empty (those rows give
