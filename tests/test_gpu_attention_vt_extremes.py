@@ -123,3 +123,47 @@ def test_one_key_far_above_the_rest(excess):
             assert m["finite"], tag
             assert m["max_abs"] <= max(ATTN_MAX_ABS, 2**-7 * peak), (tag, m)
             assert lse_err <= LSE_MAX_ABS, (tag, lse_err)
+
+
+@pytest.mark.parametrize("mode", ["random scale 12", "far key"])
+def test_planned_varlen_on_extreme_scores(mode):
+    """The planned packed launch in the d-major V form (segments of 20,000
+    and 5,000 rows at 4 heads: the device-built work list, a dynamic tail of
+    key-range pieces for the long segment's last-round tiles, the short
+    segment's V at its padded offset in the d-major copy) on random scores
+    at softmax_scale 12, and with one key 100 log2 units above the rest in
+    each segment (the overflow recompute reloads K from the segment's own
+    rows), against the oracle on sampled rows of both segments."""
+
+    lens = (20_000, 5_000)
+    St = sum(lens)
+    cu = torch.tensor([0, lens[0], St], dtype=torch.int32)
+    if mode == "random scale 12":
+        scale = 12.0
+        q, k, v = (_rand((1, St, H, D), 140 + i) for i in range(3))
+    else:
+        scale = 100.0 / (88.5 * 1.4426950408889634)
+        q = torch.zeros((1, St, H, D), dtype=torch.bfloat16)
+        q[..., 0] = 1.0
+        k = torch.zeros((1, St, H, D), dtype=torch.bfloat16)
+        k[0, 7_777, :, 0] = 88.5  # segment 0, a middle key tile
+        k[0, lens[0] + 3_001, :, 0] = 88.5  # segment 1
+        v = _rand((1, St, H, D), 143)
+    g = torch.Generator().manual_seed(144)
+    rows = torch.unique(torch.cat((torch.randperm(St, generator=g)[:160],
+                                   torch.tensor([0, lens[0] - 1, lens[0], lens[0] + 255, St - 1]))))
+    ref_o, ref_l = sdpa_rows(q, k, v, rows, scale, cu_seqlens=cu)
+    peak = max(ref_o.abs().max().item(), 1.0)
+    kw = dict(cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV), max_seqlen_q=max(lens), softmax_scale=scale)
+    print(f"case: planned varlen {lens} H={H} {mode}", flush=True)
+    out, lse = flash_attn_func(q.to(DEV), k.to(DEV), v.to(DEV), **kw)
+    torch.cuda.synchronize()
+    idx = rows.to(DEV)
+    m = error_metrics(out[:, idx].float().cpu(), ref_o)
+    l = lse[:, :, idx].double().cpu()
+    lse_err = ((l - ref_l.double()).abs() - 1e-6 * ref_l.double().abs()).max().item()
+    assert m["finite"], mode
+    assert m["max_abs"] <= max(ATTN_MAX_ABS, 2**-6 * peak), (mode, m)
+    assert lse_err <= LSE_MAX_ABS, (mode, lse_err)
+    if mode == "random scale 12":
+        assert m["relative_l2"] <= 4e-3 and m["cosine"] >= 0.99999, (mode, m)
