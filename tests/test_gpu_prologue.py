@@ -78,6 +78,29 @@ def test_head_counts_around_the_chunk_size(H):
     assert_rounding_parity(ok, qknorm_rope_reference(k, wk, cos, sin, 1e-6), ("k", H))
 
 
+@pytest.mark.parametrize("R", [128, 96, 42])
+def test_edge_magnitudes(R):
+    # rows of zeros (r = rsqrt(eps)), of tiny values (squares underflow), of
+    # large ones whose squares still sum finitely, and of ones whose squares
+    # overflow fp32 (r = 0): the fused and generic kernels against the fp32
+    # oracle, which computes the same quantities
+    B, S, H, D = 1, 8, 4, 128
+    x = _rand((B, S, H, D), 40 + R)
+    x[0, 0] = 0.0
+    x[0, 1] = x[0, 1] * 1e-30
+    x[0, 2] = x[0, 2] * 1e17
+    x[0, 3] = x[0, 3] * 1e30
+    x[0, 4, 1] = 0.0
+    x[0, 4, 2] = 3.0e38
+    w = torch.randn(D, generator=torch.Generator().manual_seed(41)).to(torch.bfloat16)
+    ang = torch.randn((S, R), generator=torch.Generator().manual_seed(42))
+    cos, sin = ang.cos(), ang.sin()
+    expect = qknorm_rope_reference(x, w, cos, sin, 1e-6)
+    assert torch.isfinite(expect.float()).all()
+    y = fused_qknorm_rope(x.to(DEV), w.to(DEV), cos.to(DEV), sin.to(DEV), 1e-6)
+    assert_rounding_parity(y, expect, ("edge", R))
+
+
 def test_q_and_k_in_one_launch_equals_two_launches():
     B, S, H, D = 1, 300, 5, 128
     q, k = _rand((B, S, H, D), 1).to(DEV), _rand((B, S, H, D), 2).to(DEV)
