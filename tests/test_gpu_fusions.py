@@ -123,6 +123,31 @@ def test_strided_rows_and_clamped_index():
     assert_parity(got, rmsnorm_modulate_reference(x, weight, scale, shift, index, 1e-5), "strided")
 
 
+@pytest.mark.parametrize("hidden", [5120, 1001])
+def test_edge_magnitudes(hidden):
+    # rows of zeros, tiny values, large ones and ones whose squares overflow
+    # fp32 (the norm factor goes to 0), on the vector and the element paths
+    rows = 6
+    x, branch, weight, (shift, scale, gate, _, _, _) = _inputs(rows, hidden, seed=12)
+    x[0, 0] = 0.0
+    x[0, 1] *= 1e-30
+    x[0, 2] *= 1e17
+    x[0, 3] *= 1e30
+    branch[0, 4] = 0.0
+    index = torch.arange(rows, dtype=torch.int64) % 9
+    expect = rmsnorm_modulate_reference(x, weight, scale, shift, index, 1e-6)
+    assert torch.isfinite(expect.float()).all()
+    got = fused_rmsnorm_modulate(x.to(DEV), weight.to(DEV), scale.to(DEV), shift.to(DEV), index.to(DEV), 1e-6)
+    assert_parity(got, expect, ("edge", hidden))
+    residual = x * 1e-3
+    rh, rn = residual_gate_rmsnorm_modulate_reference(residual, branch, gate, weight, scale, shift, index, 1e-6)
+    h, n = fused_residual_gate_rmsnorm_modulate(
+        residual.to(DEV), branch.to(DEV), gate.to(DEV), weight.to(DEV), scale.to(DEV), shift.to(DEV), index.to(DEV), 1e-6
+    )
+    assert_parity(h, rh, ("edge hidden", hidden))
+    assert_parity(n, rn, ("edge normed", hidden))
+
+
 def test_broadcast_table_rows():
     # modulation tables whose rows are one row broadcast on the device
     # (expand: row stride 0)
