@@ -23,7 +23,7 @@ import torch
 
 from h3_flash_amd import flash_attn_func
 from oracle.attention import sdpa_rows
-from oracle.metrics import ATTN_MAX_ABS, LSE_MAX_ABS, error_metrics
+from oracle.metrics import ATTN_MAX_ABS, ATTN_MEAN_ABS, LSE_MAX_ABS, error_metrics
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -167,3 +167,34 @@ def test_planned_varlen_on_extreme_scores(mode):
     assert lse_err <= LSE_MAX_ABS, (mode, lse_err)
     if mode == "random scale 12":
         assert m["relative_l2"] <= 4e-3 and m["cosine"] >= 0.99999, (mode, m)
+
+
+@pytest.mark.parametrize(
+    "B, Sq, Sk, Hh",
+    [(2, 300, 17_000, 3), (1, 5_000, 16_500, 2), (2, 16_448, 16_448, 2)],
+    ids=["cross-batch2", "cross-longer-keys", "self-batch2"],
+)
+def test_d_major_form_cross_and_batched(B, Sq, Sk, Hh):
+    """The d-major V copy per (batch, head) block (batch stride heads x 128
+    rows) and its key padding when the query and key lengths differ: batch 2,
+    few query tiles against 17,000 keys (statically split pieces), and batch
+    2 of 16,448 rows (a dynamic tail), against the oracle on sampled rows,
+    with whole tiles on V as given (no workspace) alongside."""
+
+    q = _rand((B, Sq, Hh, D), 150)
+    k = _rand((B, Sk, Hh, D), 151)
+    v = _rand((B, Sk, Hh, D), 152)
+    g = torch.Generator().manual_seed(153)
+    rows = torch.unique(torch.cat((torch.randperm(Sq, generator=g)[:128], torch.tensor([0, Sq - 1]))))
+    ref_o, ref_l = sdpa_rows(q, k, v, rows)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    for split in (True, False):
+        print(f"case: B={B} Sq={Sq} Sk={Sk} H={Hh} split_tail={split}", flush=True)
+        out, lse = flash_attn_func(qd, kd, vd, split_tail=split)
+        torch.cuda.synchronize()
+        idx = rows.to(DEV)
+        m = error_metrics(out[:, idx].float().cpu(), ref_o)
+        lse_err = (lse[:, :, idx].double().cpu() - ref_l.double()).abs().max().item()
+        tag = (B, Sq, Sk, Hh, split)
+        assert m["finite"] and m["max_abs"] <= ATTN_MAX_ABS and m["mean_abs"] <= ATTN_MEAN_ABS, (tag, m)
+        assert lse_err <= LSE_MAX_ABS, (tag, lse_err)
