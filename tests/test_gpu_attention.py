@@ -343,6 +343,48 @@ def test_small_or_misaligned_workspace_runs_whole_tiles():
             assert torch.equal(out, expect[0]) and torch.equal(lse, expect[1]), (B, S, H, offset, short)
 
 
+@pytest.mark.parametrize(
+    "B, S, H, segments",
+    [(1, 4096, 4, None), (1, 16384, 5, None), (1, 3000, 2, None), (1, 0, 4, (20_000, 5_000)), (1, 0, 2, (900, 1500, 7))],
+    ids=["static-split", "dynamic-tail-d-major", "whole", "planned-varlen", "persistent-varlen"],
+)
+def test_null_lse_gives_the_same_output(B, S, H, segments):
+    # lse = NULL through the C ABI (the caller wants no LSE): every launch
+    # kind writes the same output as with an LSE, the tail's partial LSEs
+    # still going to the workspace for the merge
+    import ctypes
+    import math
+
+    from h3_flash_amd import _ext
+
+    lib = _ext.load_library()
+    cu = None
+    if segments is not None:
+        S = sum(segments)
+        cu = torch.tensor([0, *torch.cumsum(torch.tensor(segments), 0).tolist()], dtype=torch.int32, device=DEV)
+    q, k, v = (_rand((B, S, H, 128), 80 + i).to(DEV) for i in range(3))
+    kw = {} if cu is None else dict(cu_seqlens_q=cu, cu_seqlens_k=cu, max_seqlen_q=max(segments))
+    ref_out, _ = flash_attn_func(q, k, v, **kw)
+    out = torch.full_like(q, 7.0)
+    a = _ext.AttnArgs()
+    a.abi_version = _ext.ABI_VERSION
+    a.q, a.k, a.v, a.o, a.lse = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), None
+    a.batch, a.heads, a.seqlen_q, a.seqlen_k, a.head_dim = B, H, S, S, 128
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        getattr(a, name)[:] = (S * H * 128, H * 128, 128)
+    a.softmax_scale = 1.0 / math.sqrt(128)
+    if cu is not None:
+        a.cu_seqlens_q = a.cu_seqlens_k = cu.data_ptr()
+        a.num_segments, a.max_seqlen_q = len(segments), max(segments)
+    need = lib.h3a_attn_fwd_workspace_size(ctypes.byref(a))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=DEV)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), need
+    rc = lib.h3a_attn_fwd(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream(DEV).cuda_stream))
+    assert rc == _ext.H3A_OK, _ext.last_error(lib)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_out)
+
+
 def test_workspace_plan_on_this_device():
     import ctypes
 
