@@ -641,6 +641,40 @@ def test_persistent_short_segments_on_extreme_scores(scale):
 
 
 @pytest.mark.gpu
+def test_persistent_stores_stay_inside_their_rows_and_heads():
+    """The persistent launch writes O as 16-byte stores, 32 contiguous bytes
+    of each row per store (the two half-waves exchange head dims first).
+    Into views of larger buffers filled with a sentinel: O a head slice of a
+    (1, S, H + 2, 128) tensor, the LSE a column slice; packed rows past the
+    last segment (no segment covers them) and every element outside the
+    views keep the sentinel, and the rows inside the segments equal one
+    workgroup per tile written into fresh tensors (8-byte stores)."""
+    g = torch.Generator().manual_seed(19)
+    n_seg, H, S = 60, 3, 40_000
+    lens = torch.randint(0, 600, (n_seg,), generator=g)
+    lens[0], lens[1], lens[2] = 257, 1, 0
+    cu = torch.zeros(n_seg + 1, dtype=torch.int32)
+    cu[1:] = torch.cumsum(lens, 0)
+    used = int(cu[-1])
+    assert used < S - 1000
+    q, k, v = (_rand((1, S, H, 128), 90 + i).to(DEV) for i in range(3))
+    kw = dict(cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV), max_seqlen_q=int(lens.max()))
+    sentinel = -7.25
+    big_o = torch.full((1, S, H + 2, 128), sentinel, dtype=torch.bfloat16, device=DEV)
+    big_l = torch.full((1, H, S + 64), sentinel, dtype=torch.float32, device=DEV)
+    out, lse = big_o[:, :, 1 : H + 1], big_l[:, :, 32 : S + 32]
+    flash_attn_func(q, k, v, out=out, lse=lse, **kw)
+    o_d, l_d = flash_attn_func(q, k, v, split_tail=False, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out[:, :used], o_d[:, :used])
+    assert torch.equal(lse[..., :used], l_d[..., :used])
+    assert bool((out[:, used:].float() == sentinel).all())
+    assert bool((lse[..., used:] == sentinel).all())
+    assert bool((big_o[:, :, 0].float() == sentinel).all()) and bool((big_o[:, :, H + 1].float() == sentinel).all())
+    assert bool((big_l[..., :32] == sentinel).all()) and bool((big_l[..., S + 32 :] == sentinel).all())
+
+
+@pytest.mark.gpu
 def test_persistent_cross_segments_with_empty_key_ranges():
     """Packed cross attention on the persistent launch: query and key
     segments of different lengths, some key ranges empty (those rows give
