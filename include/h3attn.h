@@ -127,7 +127,11 @@ extern "C" {
  *     counter of a persistent launch (one workgroup per CU claims tile after
  *     tile and issues each next tile's first loads during its current one;
  *     the counter is zeroed by a small kernel first). Results are
- *     bit-identical to one workgroup per tile.
+ *     bit-identical to one workgroup per tile. When the segment lengths vary
+ *     (max_seqlen_q at least 1.6 times seqlen_q / num_segments) and there
+ *     are few tiles per CU (heads x (seqlen_q / 256 + num_segments / 2) at
+ *     most 3.2 per CU, or 9 with max_seqlen_q of 2,900 or more), such calls
+ *     take the planned work list above instead.
  * With a NULL or smaller workspace every tile runs whole on V as given. The
  * results differ only by rounding. Calls sharing one workspace must be
  * ordered (same stream).

@@ -345,8 +345,15 @@ def test_small_or_misaligned_workspace_runs_whole_tiles():
 
 @pytest.mark.parametrize(
     "B, S, H, segments",
-    [(1, 4096, 4, None), (1, 16384, 5, None), (1, 3000, 2, None), (1, 0, 4, (20_000, 5_000)), (1, 0, 2, (900, 1500, 7))],
-    ids=["static-split", "dynamic-tail-d-major", "whole", "planned-varlen", "persistent-varlen"],
+    [
+        (1, 4096, 4, None),
+        (1, 16384, 5, None),
+        (1, 3000, 2, None),
+        (1, 0, 4, (20_000, 5_000)),
+        (1, 0, 2, (1500, 1400, 1207)),
+        (1, 0, 5, (3000,) + (40,) * 30),
+    ],
+    ids=["static-split", "dynamic-tail-d-major", "whole", "planned-varlen", "persistent-varlen", "planned-short-varlen"],
 )
 def test_null_lse_gives_the_same_output(B, S, H, segments):
     # lse = NULL through the C ABI (the caller wants no LSE): every launch
@@ -428,6 +435,62 @@ def test_workspace_plan_on_this_device():
         # 201 tiles (78%): whole; the d-major V pads 51,201 keys to 51,264
         assert need(1, 51201, 1) == need(1, 51264, 1) == vt(1, 51264, 1) == 128 * 51264 * 2
     assert need(1, 64, 1) == 0  # one key tile: nothing to split, no d-major V
+
+
+def _varlen_workspace(lens, H):
+    import ctypes
+
+    from h3_flash_amd import _ext
+
+    S = int(sum(lens))
+    a = _ext.AttnArgs()
+    a.abi_version = _ext.ABI_VERSION
+    a.q = a.k = a.v = a.o = 1 << 20
+    a.batch, a.heads, a.seqlen_q, a.seqlen_k, a.head_dim = 1, H, S, S, 128
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride"):
+        getattr(a, name)[:] = (S * H * 128, H * 128, 128)
+    a.lse_stride[:] = (H * S, S)
+    a.softmax_scale = 0.088
+    a.cu_seqlens_q = a.cu_seqlens_k = 1 << 20
+    a.num_segments, a.max_seqlen_q = len(lens), int(max(lens))
+    return _ext.load_library().h3a_attn_fwd_workspace_size(ctypes.byref(a))
+
+
+def test_short_segments_route_by_length_spread():
+    """Packed calls whose longest segment has fewer than 4,096 rows run on
+    the persistent launch (its 256-byte tile counter) unless their lengths
+    vary (the longest at least 1.6 times the mean) and there are few tiles
+    per CU (at most 3.2 rounds, or 9 with segments of 2,900 rows or more):
+    then the planned list (no tiles past a segment's rows, longest segments
+    first, the last round as key-range pieces) balances the CUs. The
+    workspace each asks for tells the two apart. The planned route then
+    matches the oracle on sampled rows of its segments."""
+
+    if torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the rule's rounds are stated for a 256-CU part")
+    g = torch.Generator().manual_seed(23)
+    ragged_long = torch.randint(1, 4096, (40,), generator=g).tolist()  # mean ~2,000: 6.6 rounds at H5
+    ragged_short = torch.randint(1, 2049, (60,), generator=g).tolist()  # mean ~1,000: 5.3 rounds at H5
+    assert _varlen_workspace([1024] * 48, 5) == 256  # equal lengths: persistent
+    assert _varlen_workspace([2048] * 8, 5) == 256  # equal lengths, 1.3 rounds: persistent
+    assert _varlen_workspace(ragged_short, 5) == 256  # varied, 5.3 rounds of short tiles: persistent
+    assert _varlen_workspace(ragged_long, 5) > 256  # varied, 6.6 rounds, tiles up to 64 key tiles: planned
+    tiny = [3000] + [40] * 30
+    assert _varlen_workspace(tiny, 5) > 256  # varied, 0.6 rounds: planned
+
+    for lens, H, seed in ((tiny, 5, 31), ([3900, 40, 2500, 7, 1200, 3100, 64, 900], 2, 32)):
+        assert _varlen_workspace(lens, H) > 256
+        cu = torch.tensor([0, *torch.cumsum(torch.tensor(lens), 0).tolist()], dtype=torch.int32)
+        S = int(cu[-1])
+        q, k, v = (_rand((1, S, H, 128), seed * 3 + i) for i in range(3))
+        out, lse = flash_attn_func(
+            q.to(DEV), k.to(DEV), v.to(DEV), cu_seqlens_q=cu.to(DEV), cu_seqlens_k=cu.to(DEV), max_seqlen_q=max(lens)
+        )
+        torch.cuda.synchronize()
+        rows = _sample_rows(S, 200, seed, extra=[int(c) for c in cu[1:-1]])
+        ref_o, ref_l = sdpa_rows(q, k, v, rows, cu_seqlens=cu)
+        idx = rows.to(DEV)
+        assert_parity(out[:, idx].cpu(), lse[:, :, idx].cpu(), ref_o, ref_l, ("planned short", len(lens), H))
 
 
 def test_unsupported_requests_raise():
@@ -576,7 +639,7 @@ def test_full_size_properties(name):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("seed,n_seg,max_len", [(0, 300, 2048), (1, 700, 512), (2, 40, 300), (3, 90, 4000)])
+@pytest.mark.parametrize("seed,n_seg,max_len", [(0, 300, 2048), (1, 700, 512), (2, 400, 300), (3, 200, 4000)])
 def test_persistent_short_segments_match_dispatch_order(seed, n_seg, max_len):
     """Packed short segments (fewer than 4,096 rows) with a workspace run on
     persistent workgroups that claim tiles from a counter and prefetch each
@@ -617,7 +680,7 @@ def test_persistent_short_segments_on_extreme_scores(scale):
     tile): bit for bit equal to one workgroup per tile, and sampled segments
     within the extreme-scale bounds of the oracle."""
     g = torch.Generator().manual_seed(int(scale))
-    n_seg, H = 120, 2
+    n_seg, H = 200, 2
     lens = torch.randint(1, 1500, (n_seg,), generator=g)
     cu = torch.zeros(n_seg + 1, dtype=torch.int32)
     cu[1:] = torch.cumsum(lens, 0)

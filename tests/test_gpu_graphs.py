@@ -88,18 +88,20 @@ def test_prologue_attention_and_fusion_replay_in_a_graph():
 
 @pytest.mark.parametrize("heads", [5, 40])
 def test_persistent_short_segment_launch_replays_in_a_graph(heads):
-    # a packed launch whose longest segment is under 4,096 rows runs one
-    # workgroup per CU that claims tiles from a counter (reset by a kernel
-    # recorded in the graph); the segmentation changes between replays, the
-    # number of segments (and max_seqlen_q) staying what was captured
-    rows, D, max_q = 9000, 128, 3000
+    # a packed launch whose longest segment is under 4,096 rows, the longest
+    # at most 1.6 times the mean (12,000 rows in 5 segments of at most 3,000),
+    # runs one workgroup per CU that claims tiles from a counter (reset by a
+    # kernel recorded in the graph); the segmentation changes between
+    # replays, the number of segments (and max_seqlen_q) staying what was
+    # captured
+    rows, D, max_q = 12000, 128, 3000
     q, k, v = (torch.empty((1, rows, heads, D), dtype=torch.bfloat16, device=DEV) for _ in range(3))
-    segmentations = (
-        [0, 1024, 2048, 5000, 8000, 9000],
-        [0, 3000, 6000, 9000, 9000, 9000],
-        [0, 1, 2000, 4500, 7000, 9000],
-        [0, 0, 2999, 5998, 8997, 9000],
-        [0, 700, 1400, 4000, 6500, 9000],
+    segmentations = (  # every row in a segment, as the eager comparison needs
+        [0, 3000, 6000, 9000, 12000, 12000],
+        [0, 1024, 3500, 6000, 9000, 12000],
+        [0, 1, 3000, 6000, 9000, 12000],
+        [0, 0, 3000, 6000, 9000, 12000],
+        [0, 700, 3700, 6500, 9500, 12000],
     )
     cu = torch.tensor(segmentations[0], dtype=torch.int32, device=DEV)
 
