@@ -141,22 +141,6 @@ __device__ __forceinline__ int lane_from_hw() {
     return l;
 }
 
-// One query tile (chunk < 0), or key-range piece `chunk` of `chunks` of a
-// tile. A piece with a workspace slot (slot >= 0) writes normalised fp32
-// partial O and LSE there for the merge; a whole tile, or a piece covering
-// the tile's whole key range (slot < 0), writes O and LSE. All waves of the
-// workgroup call it with the same arguments; it returns with no LDS DMA in
-// flight.
-// kWide: views whose span reaches 2^31 bytes. Their K / V buffer resources
-// are rebased as the key loop moves on (a window of kWindowRows rows), so
-// 32-bit offsets never cover more than one window. Shorter views keep one
-// resource per view: the rebase needs scalar registers this kernel does not
-// have to spare, so it is not paid where it is not needed.
-// kVT: V is read from a d-major copy (p.vt: per (batch, head) 128 rows of
-// keys, zero past the last key), so each PV fragment is one ds_read_b128
-// instead of two transpose reads. The K rows of every 16-key group are then
-// taken in the order that swaps bits 2 and 3 of the key index (keyperm), so
-// that the eight keys a lane holds in P^T are consecutive.
 // Normalised O of head-dim blocks 4db + 2m and 4db + 2m + 1 (8 dims each)
 // from a lane's accumulator block db: the lower half-wave holds dims 0-3 of
 // each block, the upper one dims 4-7, of the same row. One
@@ -189,6 +173,22 @@ __device__ __forceinline__ char* attn_lds() {
     return smem;
 }
 
+// One query tile (chunk < 0), or key-range piece `chunk` of `chunks` of a
+// tile. A piece with a workspace slot (slot >= 0) writes normalised fp32
+// partial O and LSE there for the merge; a whole tile, or a piece covering
+// the tile's whole key range (slot < 0), writes O and LSE. All waves of the
+// workgroup call it with the same arguments; it returns with no LDS DMA in
+// flight.
+// kWide: views whose span reaches 2^31 bytes. Their K / V buffer resources
+// are rebased as the key loop moves on (a window of kWindowRows rows), so
+// 32-bit offsets never cover more than one window. Shorter views keep one
+// resource per view: the rebase needs scalar registers this kernel does not
+// have to spare, so it is not paid where it is not needed.
+// kVT: V is read from a d-major copy (p.vt: per (batch, head) 128 rows of
+// keys, zero past the last key), so each PV fragment is one ds_read_b128
+// instead of two transpose reads. The K rows of every 16-key group are then
+// taken in the order that swaps bits 2 and 3 of the key index (keyperm), so
+// that the eight keys a lane holds in P^T are consecutive.
 // kPersist (packed launches without a work list, neither wide nor d-major
 // V): qcarry holds Q across calls; `prefetched` says that the previous call
 // already issued this tile's Q loads and its first K / V DMA, and next_tile
