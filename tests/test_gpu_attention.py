@@ -493,6 +493,51 @@ def test_short_segments_route_by_length_spread():
         assert_parity(out[:, idx].cpu(), lse[:, :, idx].cpu(), ref_o, ref_l, ("planned short", len(lens), H))
 
 
+def test_planned_short_cross_segments_with_empty_ranges():
+    """Packed cross attention whose short query segments vary in length with
+    few tiles per CU takes the planned list: query and key segments of
+    different lengths, some key ranges empty (O = 0, LSE = -inf) and some
+    query ranges empty. Against one workgroup per tile within the path's
+    tolerance, and sampled rows of every non-empty segment against the
+    oracle."""
+    g = torch.Generator().manual_seed(37)
+    n_seg, H = 24, 2
+    lq = torch.randint(0, 3500, (n_seg,), generator=g)
+    lk = torch.randint(0, 5000, (n_seg,), generator=g)
+    lq[0], lk[0] = 3500, 0  # the longest query segment sees no keys
+    lq[3], lq[7] = 0, 1
+    lk[5] = 0
+    cq = torch.zeros(n_seg + 1, dtype=torch.int32)
+    ck = torch.zeros(n_seg + 1, dtype=torch.int32)
+    cq[1:], ck[1:] = torch.cumsum(lq, 0), torch.cumsum(lk, 0)
+    Sq, Sk = int(cq[-1]), int(ck[-1])
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert _varlen_workspace(lq.tolist(), H) > 256  # the planned list, not the persistent counter
+    q = _rand((1, Sq, H, 128), 41).to(DEV)
+    k = _rand((1, Sk, H, 128), 42).to(DEV)
+    v = _rand((1, Sk, H, 128), 43).to(DEV)
+    kw = dict(cu_seqlens_q=cq.to(DEV), cu_seqlens_k=ck.to(DEV), max_seqlen_q=int(lq.max()))
+    out, lse = flash_attn_func(q, k, v, **kw)
+    o_d, l_d = flash_attn_func(q, k, v, split_tail=False, **kw)
+    torch.cuda.synchronize()
+    a, b = int(cq[0]), int(cq[1])
+    assert torch.count_nonzero(out[:, a:b]).item() == 0
+    assert bool(torch.isneginf(lse[..., a:b]).all())
+    live = torch.isfinite(l_d)
+    assert torch.equal(live, torch.isfinite(lse))
+    assert_parity(out.cpu(), torch.where(live, lse, 0).cpu(), o_d.float().cpu(), torch.where(live, l_d, 0).cpu(),
+                  "planned vs one workgroup per tile")
+    for s_ in range(n_seg):
+        qa, qb, ka, kb = int(cq[s_]), int(cq[s_ + 1]), int(ck[s_]), int(ck[s_ + 1])
+        if qb == qa or kb == ka:
+            continue
+        rows = torch.unique(torch.tensor([qa, qb - 1, (qa + qb) // 2]))
+        ref_o, ref_l = sdpa_reference(q[:, qa:qb].cpu(), k[:, ka:kb].cpu(), v[:, ka:kb].cpu())
+        loc = rows - qa
+        assert_parity(out[:, rows.to(DEV)].cpu(), lse[..., rows.to(DEV)].cpu(), ref_o[:, loc], ref_l[..., loc],
+                      ("segment", s_))
+
+
 def test_unsupported_requests_raise():
     q = _rand((1, 8, 2, 128), 15).to(DEV)
     with pytest.raises(RuntimeError, match="non-causal"):
