@@ -375,6 +375,17 @@ int h3a_attn_fwd_noalloc(const h3a_attn_args* a, void* stream) {
         return fail(H3A_EINVAL, "h3a_attn_fwd_noalloc: the launch needs %lld bytes of scratch, the static scratch holds %lld",
                     (long long)plan.workspace_bytes, (long long)h3a::kStaticScratchBytes);
     if (plan.split_n != 0) apply_plan(p, plan, scratch);
+    // Packed short segments: the persistent launch, its tile counter in the
+    // scratch's first 256 bytes (no split plan uses the scratch then; its
+    // zeroing kernel is part of the launch). The planned list's partial
+    // results would not fit, so varied lengths take this launch too.
+    if (plan.split_n == 0 && a->cu_seqlens_q != nullptr && a->max_seqlen_q <= h3a::attn_fwd_persist_max_rows()) {
+        const int cus = device_cus();
+        if (cus > 0) {
+            p.persist_queue = (int*)scratch;
+            p.persist_blocks = cus;
+        }
+    }
     e = h3a::launch_attn_fwd(p, (hipStream_t)stream);
     if (e != hipSuccess) return fail(H3A_ELAUNCH, "h3a_attn_fwd_noalloc: launch failed: %s", hipGetErrorString(e));
     return H3A_OK;

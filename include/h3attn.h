@@ -184,8 +184,10 @@ H3A_API int64_t h3a_attn_fwd_workspace_size(const h3a_attn_args *args);
  * runs on holds until the process ends; its address is looked up once per
  * device. The split plan is fitted to that array (fewer key-range pieces,
  * or none), so any problem size runs; a plan that could not be fitted would
- * be rejected with H3A_EINVAL. The call allocates nothing, issues no memset
- * and does not synchronise.
+ * be rejected with H3A_EINVAL. Packed calls with max_seqlen_q below 4,096
+ * run the persistent launch, its tile counter in the same array (also those
+ * of varied lengths, whose planned list would not fit). The call allocates
+ * nothing, issues no memset and does not synchronise.
  *
  * All calls on one GPU share its array: calls that overlap on one GPU (on
  * different streams, or from different threads without ordering) race on
