@@ -141,28 +141,6 @@ __device__ __forceinline__ int lane_from_hw() {
     return l;
 }
 
-// Normalised O of head-dim blocks 4db + 2m and 4db + 2m + 1 (8 dims each)
-// from a lane's accumulator block db: the lower half-wave holds dims 0-3 of
-// each block, the upper one dims 4-7, of the same row. One
-// v_permlane32_swap per dword leaves block 4db + 2m whole (16 bytes) in the
-// lower lane and block 4db + 2m + 1 in the upper one.
-__device__ __forceinline__ i32x4 swapped_chunk(const f32x16& acc, float inv, int m) {
-    const int ie = 2 * m, io = 2 * m + 1;
-    const uint32_t e0 = pack_bf16x2(acc[ie * 4 + 0] * inv, acc[ie * 4 + 1] * inv);
-    const uint32_t e1 = pack_bf16x2(acc[ie * 4 + 2] * inv, acc[ie * 4 + 3] * inv);
-    const uint32_t o0 = pack_bf16x2(acc[io * 4 + 0] * inv, acc[io * 4 + 1] * inv);
-    const uint32_t o1 = pack_bf16x2(acc[io * 4 + 2] * inv, acc[io * 4 + 3] * inv);
-    // Lower lanes keep e and take the upper lanes' e; upper lanes take the
-    // lower lanes' o and keep o.
-    const auto s0 = __builtin_amdgcn_permlane32_swap(e0, o0, false, false);
-    const auto s1 = __builtin_amdgcn_permlane32_swap(e1, o1, false, false);
-    return i32x4{(int)s0[0], (int)s1[0], (int)s0[1], (int)s1[1]};
-}
-
-// The 8-dim block that swapped_chunk(acc[db], inv, m) holds in a lane of
-// half-wave hi.
-__device__ __forceinline__ int swapped_block(int db, int m, int hi) { return 4 * db + 2 * m + hi; }
-
 // The launch arguments as the tail loop reads them: where they lie (the
 // kernel-argument segment, through the scalar cache).
 using KernArgs = const __attribute__((address_space(4))) AttnParams;
@@ -880,32 +858,58 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
         if (hi == 0) p.ws_lse[(int64_t)slot * kBM + row] = lse;
         return false;
     }
+    if constexpr (kPersist) {
+        // Short tiles store O through the wave's 2 KB of V stage 3 (free
+        // now: its last reader was the final step's PV, before that step's
+        // barrier; the prefetch fills other stages, and the next tile
+        // writes it only after its own barriers). A lane holds four dims of
+        // every 8-dim block of one row; in four passes of 32 dims each, the
+        // lanes write their pieces there, then each lane reads back 16
+        // bytes, four lanes one row's 64 contiguous bytes, and stores them:
+        // 128 L2 requests per wave and tile against 512 for 8-byte stores
+        // straight from the accumulators (48 x 1,024-row segments ran 9%
+        // faster, 96 x 512 15%). Long tiles store once per hundreds of key
+        // tiles, and the dense workloads measured the same either way, so
+        // they keep the direct stores. One wave's LDS accesses run in
+        // order, so each pass reads what it wrote and the next pass writes
+        // over what was read. 16-byte chunks are XOR-swizzled by row pair:
+        // the reads are bank-conflict free.
+        typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
+        typedef __attribute__((address_space(3))) i32x4 lds_i32x4;
+        lds_char* const staged = (lds_char*)(vst + 3 * kTile) + wave * 32 * 64;
+        char* const ob0 = (char*)p.o + 2 * (b * p.o_sb + h * p.o_sh) + (int64_t)q0 * p.o_rs;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                i32x2 w;
+                w.x = (int)pack_bf16x2(oacc[db][i * 4 + 0] * inv, oacc[db][i * 4 + 1] * inv);
+                w.y = (int)pack_bf16x2(oacc[db][i * 4 + 2] * inv, oacc[db][i * 4 + 3] * inv);
+                *(lds_i32x2*)(staged + l32 * 64 + (((i ^ ((l32 >> 1) & 3)) << 4) | (hi << 3))) = w;
+            }
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                const int row = (lane >> 2) + 16 * k, c = lane & 3;
+                const i32x4 v = *(const lds_i32x4*)(staged + row * 64 + ((c ^ ((row >> 1) & 3)) << 4));
+                const int grow = m0 + wave * 32 + row;
+                if (grow < sq) *(i32x4*)(ob0 + (int64_t)grow * p.o_rs + db * 64 + c * 16) = v;
+            }
+        }
+        if (emq < sq && p.lse != nullptr && hi == 0) p.lse[b * p.lse_sb + h * p.lse_sh + q0 + emq] = lse;
+        return pref;
+    }
     if (emq < sq) {
         char* ob = (char*)p.o + 2 * (b * p.o_sb + h * p.o_sh) + (int64_t)(q0 + emq) * p.o_rs;
-        if constexpr (kPersist) {
-            // Short tiles: 16-byte stores of whole head-dim blocks, 32
-            // contiguous bytes of every row per store (half as many L2
-            // requests, each twice as large: 48 x 1,024-row segments ran
-            // 6% faster, 96 x 512 10%). Long tiles store once per
-            // hundreds of key tiles, and the dense workloads measured the
-            // same either way, so they keep the 8-byte stores.
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
+        for (int db = 0; db < 4; ++db)
 #pragma unroll
-                for (int m = 0; m < 2; ++m)
-                    *(i32x4*)(ob + swapped_block(db, m, hi) * 16) = swapped_chunk(oacc[db], inv, m);
-        } else {
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int d = db * 32 + i * 8 + hi * 4;
-                    i32x2 w;
-                    w.x = (int)pack_bf16x2(oacc[db][i * 4 + 0] * inv, oacc[db][i * 4 + 1] * inv);
-                    w.y = (int)pack_bf16x2(oacc[db][i * 4 + 2] * inv, oacc[db][i * 4 + 3] * inv);
-                    *(i32x2*)(ob + d * 2) = w;
-                }
-        }
+            for (int i = 0; i < 4; ++i) {
+                const int d = db * 32 + i * 8 + hi * 4;
+                i32x2 w;
+                w.x = (int)pack_bf16x2(oacc[db][i * 4 + 0] * inv, oacc[db][i * 4 + 1] * inv);
+                w.y = (int)pack_bf16x2(oacc[db][i * 4 + 2] * inv, oacc[db][i * 4 + 3] * inv);
+                *(i32x2*)(ob + d * 2) = w;
+            }
         if (p.lse != nullptr && hi == 0) p.lse[b * p.lse_sb + h * p.lse_sh + q0 + emq] = lse;
     }
     return pref;
