@@ -840,44 +840,26 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
     // Query row of the lane: the wide forms take it from the lane taken
     // after the key loop rather than hold it across the loop.
     const int emq = kWide ? m0 + wave * 32 + l32 : mq;
-    if (slot >= 0) {
-        // Partial result of a key-range piece: normalised O in bf16 (as the
-        // output itself is rounded) and the LSE in fp32.
-        const int row = wave * 32 + l32;
-        uint16_t* wo = p.ws_o + ((int64_t)slot * kBM + row) * kD;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int d = db * 32 + i * 8 + hi * 4;
-                i32x2 w;
-                w.x = (int)pack_bf16x2(oacc[db][i * 4 + 0] * inv, oacc[db][i * 4 + 1] * inv);
-                w.y = (int)pack_bf16x2(oacc[db][i * 4 + 2] * inv, oacc[db][i * 4 + 3] * inv);
-                *(i32x2*)(wo + d) = w;
-            }
-        if (hi == 0) p.ws_lse[(int64_t)slot * kBM + row] = lse;
-        return false;
-    }
-    if constexpr (kPersist) {
-        // Short tiles store O through the wave's 2 KB of V stage 3 (free
-        // now: its last reader was the final step's PV, before that step's
-        // barrier; the prefetch fills other stages, and the next tile
-        // writes it only after its own barriers). A lane holds four dims of
-        // every 8-dim block of one row; in four passes of 32 dims each, the
-        // lanes write their pieces there, then each lane reads back 16
-        // bytes, four lanes one row's 64 contiguous bytes, and stores them:
-        // 128 L2 requests per wave and tile against 512 for 8-byte stores
-        // straight from the accumulators (48 x 1,024-row segments ran 9%
-        // faster, 96 x 512 15%). Long tiles store once per hundreds of key
-        // tiles, and the dense workloads measured the same either way, so
-        // they keep the direct stores. One wave's LDS accesses run in
-        // order, so each pass reads what it wrote and the next pass writes
-        // over what was read. 16-byte chunks are XOR-swizzled by row pair:
-        // the reads are bank-conflict free.
+    // This wave's 32 rows of O, normalised to bf16, written through its
+    // 2 KB of V stage 3. The stage is free here: its last reader, the final
+    // step's PV, finished before that step's barrier; a persistent launch's
+    // prefetch fills the other stages; a later call writes it only in its
+    // first main-loop step, and there each wave's DMA fills exactly its own
+    // 2 KB (eight 256-byte key rows, or sixteen 128-byte dim rows of a
+    // d-major tile) after its own reads here. A lane holds four dims of
+    // every 8-dim block of one row; in four passes of 32 dims the lanes
+    // write their pieces, then each reads back 16 bytes, four lanes one
+    // row's 64 contiguous bytes, and stores them: 128 L2 requests per wave
+    // instead of 512 for 8-byte stores straight from the accumulators
+    // (short tiles ran up to 15% faster). One wave's LDS accesses run in
+    // order, so each pass reads what it wrote and the next writes over what
+    // was read. 16-byte chunks are XOR-swizzled by row pair: the reads are
+    // bank-conflict free. Row r of the wave goes to base + r * row_bytes
+    // when r < rows.
+    auto staged_store = [&](char* base, int64_t row_bytes, int rows) __attribute__((always_inline)) {
         typedef __attribute__((address_space(3))) i32x2 lds_i32x2;
         typedef __attribute__((address_space(3))) i32x4 lds_i32x4;
         lds_char* const staged = (lds_char*)(vst + 3 * kTile) + wave * 32 * 64;
-        char* const ob0 = (char*)p.o + 2 * (b * p.o_sb + h * p.o_sh) + (int64_t)q0 * p.o_rs;
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
 #pragma unroll
@@ -891,27 +873,20 @@ __device__ __forceinline__ bool attn_tile(Params& p, int tile, int chunk, int ch
             for (int k = 0; k < 2; ++k) {
                 const int row = (lane >> 2) + 16 * k, c = lane & 3;
                 const i32x4 v = *(const lds_i32x4*)(staged + row * 64 + ((c ^ ((row >> 1) & 3)) << 4));
-                const int grow = m0 + wave * 32 + row;
-                if (grow < sq) *(i32x4*)(ob0 + (int64_t)grow * p.o_rs + db * 64 + c * 16) = v;
+                if (row < rows) *(i32x4*)(base + (int64_t)row * row_bytes + db * 64 + c * 16) = v;
             }
         }
-        if (emq < sq && p.lse != nullptr && hi == 0) p.lse[b * p.lse_sb + h * p.lse_sh + q0 + emq] = lse;
-        return pref;
+    };
+    if (slot >= 0) {
+        // Partial result of a key-range piece: normalised O in bf16 (as the
+        // output itself is rounded) and the LSE in fp32, every row.
+        staged_store((char*)(p.ws_o + ((int64_t)slot * kBM + wave * 32) * kD), kD * 2, 32);
+        if (hi == 0) p.ws_lse[(int64_t)slot * kBM + wave * 32 + l32] = lse;
+        return false;
     }
-    if (emq < sq) {
-        char* ob = (char*)p.o + 2 * (b * p.o_sb + h * p.o_sh) + (int64_t)(q0 + emq) * p.o_rs;
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int d = db * 32 + i * 8 + hi * 4;
-                i32x2 w;
-                w.x = (int)pack_bf16x2(oacc[db][i * 4 + 0] * inv, oacc[db][i * 4 + 1] * inv);
-                w.y = (int)pack_bf16x2(oacc[db][i * 4 + 2] * inv, oacc[db][i * 4 + 3] * inv);
-                *(i32x2*)(ob + d * 2) = w;
-            }
-        if (p.lse != nullptr && hi == 0) p.lse[b * p.lse_sb + h * p.lse_sh + q0 + emq] = lse;
-    }
+    const int wrow = m0 + wave * 32;  // the wave's first query row
+    staged_store((char*)p.o + 2 * (b * p.o_sb + h * p.o_sh) + (int64_t)(q0 + wrow) * p.o_rs, p.o_rs, sq - wrow);
+    if (emq < sq && p.lse != nullptr && hi == 0) p.lse[b * p.lse_sb + h * p.lse_sh + q0 + emq] = lse;
     return pref;
 }
 
